@@ -1,0 +1,164 @@
+/*
+ * tachyon_sampler.h - C ABI of the MI355X batched token-sampling path.
+ *
+ * One call samples the next token of every row of a [rows x row_stride] f32
+ * logits matrix that already sits in device memory (HBM).  Per row it runs
+ * the pipeline of Tachyon's CPU sampler (src/sampler.rs) plus the extension
+ * fields this path adds:
+ *
+ *   repetition / presence / frequency penalties from the row's history
+ *   -> window of best candidates (top_n, or the 30*T cutoff when there is no
+ *      top-k) -> packed-mask filter with the reference's window/fallback rule
+ *   -> truncate to top-k -> probabilities exp((l - l0) / T) -> min-p
+ *   -> top-p -> inverse-CDF draw with the caller's uniform
+ *   -> optional logprob of the pick and the top-n alternatives (raw logits).
+ *
+ * Every array argument is a DEVICE pointer.  Work is queued on the caller's
+ * HIP stream and is asynchronous; results are valid once the stream reaches
+ * the call.  The context is not re-entrant: one context per stream, one call
+ * at a time (as with the reference's GpuBackend, src/gpu/mod.rs:440-442).
+ *
+ * Errors follow the reference's FFI convention (src/gpu/shim.m:130,
+ * src/gpu/mod.rs:467-480): a NULL handle or a nonzero int status, and a
+ * NUL-terminated message written into the caller's (err, errlen) buffer.
+ * "Nothing allowed" is not an error: such a row returns the argmax of its raw
+ * logits, as the reference does (src/sampler.rs:139-141).
+ */
+#ifndef TACHYON_SAMPLER_H
+#define TACHYON_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Most alternatives a row may ask logprobs for (src/server.rs:625-634 caps
+ * `top_logprobs` at 20). */
+#define TSM_MAX_LOGPROBS 20u
+/* Longest history a row may carry (token counts are kept in 16 bits). */
+#define TSM_MAX_HISTORY 65535u
+/* Largest vocabulary (usable ids per row) a context accepts. */
+#define TSM_MAX_VOCAB (1u << 22)
+
+/* tsm_row_params.flags */
+#define TSM_ROW_CONSTRAINED 1u /* sample_with(): the row's mask bits apply   */
+#define TSM_ROW_LOGPROBS    2u /* report logprob of the pick + n_logprobs   */
+
+/*
+ * Per-row sampling settings.  The first five fields are Tachyon's
+ * SamplerConfig (src/sampler.rs:6-17) minus the seed: the RNG stays with the
+ * host-side Sampler, which passes one uniform per row instead.  The three
+ * penalty/min-p fields are extensions; their zero values reproduce the
+ * reference exactly.  Layout is fixed: 40 bytes, 4-byte aligned.
+ */
+typedef struct tsm_row_params {
+    float    temperature;        /* <= 0: greedy (sampler.rs:8, :161)            */
+    uint32_t top_k;              /* 0: no limit (sampler.rs:10, :179)            */
+    float    top_p;              /* >= 1: off (sampler.rs:235)                   */
+    float    repetition_penalty; /* 1: off (sampler.rs:165-175)                 */
+    float    presence_penalty;   /* extension, 0: off                            */
+    float    frequency_penalty;  /* extension, 0: off                            */
+    float    min_p;              /* extension, <= 0: off                         */
+    uint32_t flags;              /* TSM_ROW_* bits                               */
+    uint32_t n_logprobs;         /* alternatives when TSM_ROW_LOGPROBS, <= 20    */
+    uint32_t reserved;           /* must be 0                                    */
+} tsm_row_params;
+
+/*
+ * One step's inputs.  Row r's logits are logits[r*row_stride .. +usable]
+ * (src/scheduler.rs:625-626,652: usable = min(tokenizer.len(), vocab)).
+ * History is CSR: row r's ids are hist_ids[hist_offsets[r] ..
+ * hist_offsets[r+1]) (the `recent` slice of src/scheduler.rs:653); ids >=
+ * usable are ignored, as the reference's `buf.get_mut(id)` ignores them.
+ * The mask is packed LSB-first: bit b of word w of row r allows token 32w+b;
+ * bits at or above `usable` must be 0.
+ */
+typedef struct tsm_batch {
+    const float*          logits;       /* [rows][row_stride]                   */
+    uint32_t              rows;
+    uint32_t              row_stride;   /* elements; >= usable                  */
+    uint32_t              usable;       /* ids considered per row; >= 1         */
+    uint32_t              mask_stride;  /* u32 words per mask row               */
+    const tsm_row_params* params;       /* [rows]                               */
+    const uint32_t*       hist_ids;     /* CSR values, NULL if every row empty  */
+    const uint32_t*       hist_offsets; /* [rows+1], NULL if every row empty    */
+    const uint32_t*       mask;         /* [rows][mask_stride], NULL if no row
+                                           sets TSM_ROW_CONSTRAINED             */
+    const float*          uniforms;     /* [rows], each in [0, 1)               */
+} tsm_batch;
+
+/* One step's outputs.  `token` is required; every other pointer may be NULL. */
+typedef struct tsm_outputs {
+    uint32_t* token;        /* [rows] picked id                                  */
+    float*    logprob;      /* [rows] raw log-softmax of the pick
+                               (sampler::logprobs, src/sampler.rs:297-312)     */
+    uint32_t* top_ids;      /* [rows][top_stride] best raw ids, ties -> lower id */
+    float*    top_logprobs; /* [rows][top_stride] their log-softmax values       */
+    uint32_t  top_stride;   /* >= every row's n_logprobs when top_* are given    */
+    uint32_t  reserved;
+    float*    prob;         /* [rows] probability of the pick under the final,
+                               normalised distribution (p_tok / mass)           */
+    uint32_t* keep;         /* [rows] size of the kept set the draw used         */
+} tsm_outputs;
+
+typedef struct tsm_ctx tsm_ctx;
+
+/*
+ * Creates a sampling context on HIP device `device` for calls with up to
+ * `max_rows` rows of up to `max_vocab` usable ids; all device scratch is
+ * allocated here, none per call.  Returns NULL and fills `err` on failure.
+ * Replaces: the per-sequence scratch of Sampler::new (src/sampler.rs:63-73);
+ * FFI shape follows tm_create (src/gpu/mod.rs:117-123).
+ */
+tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab,
+                    char* err, size_t errlen);
+
+/* Frees a context (NULL is a no-op).  Replaces tm_destroy (src/gpu/mod.rs:124). */
+void tsm_destroy(tsm_ctx* ctx);
+
+/*
+ * Samples one token per row.  `stream` is a hipStream_t (NULL: the null
+ * stream).  Returns 0, or nonzero with a message in `err` when an argument is
+ * invalid (checked on the host before anything is queued).
+ * Replaces: the per-row loop of src/scheduler.rs:638-675, i.e. for each row
+ * Sampler::sample / Sampler::sample_with (src/sampler.rs:77-97) followed by
+ * sampler::logprobs (src/sampler.rs:297-312).
+ */
+int tsm_sample(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
+               const tsm_outputs* out, char* err, size_t errlen);
+
+/*
+ * Writes each row's final distribution, best first, as normalised (id, p)
+ * pairs: row r gets min(keep, dist_stride) pairs in dist_ids/dist_probs
+ * [r*dist_stride ..] and its full kept count in keep[r].  No draw is made;
+ * `batch->uniforms` may be NULL and TSM_ROW_CONSTRAINED is ignored, as
+ * Sampler::distribution takes no constraint.
+ * Replaces: Sampler::distribution (src/sampler.rs:102-116), used by
+ * speculative decoding (src/speculative.rs:96-97, :306).
+ */
+int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
+                     uint32_t* dist_ids, float* dist_probs,
+                     uint32_t dist_stride, uint32_t* keep,
+                     char* err, size_t errlen);
+
+/*
+ * Waits for the context's last call and returns its device-side status:
+ * 0 when every row was sampled by the specified rule, otherwise TSM_STATUS_*
+ * bits (e.g. a history row longer than TSM_MAX_HISTORY, whose counts are
+ * then capped).  Clears the status.
+ */
+#define TSM_STATUS_HISTORY_TOO_LONG 1u
+#define TSM_STATUS_BAD_PARAMS       2u
+#define TSM_STATUS_DIST_TRUNCATED   4u
+int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);
+
+/* Library version string, e.g. "tachyon-sampler 0.1 gfx950". */
+const char* tsm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TACHYON_SAMPLER_H */

@@ -1,0 +1,297 @@
+"""ctypes binding of oracle/libtachyon_oracle.so (TEST INFRASTRUCTURE ONLY).
+
+The C++ oracle restates /root/reference/src/sampler.rs; see
+oracle/tachyon_oracle.cpp.  Used by tests/, smoke() and bench.py's
+cpu_baseline leg as the checker, never by the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtachyon_oracle.so")
+
+c_f32p = ctypes.POINTER(ctypes.c_float)
+c_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+class OrConfig(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_uint32),
+        ("top_p", ctypes.c_float),
+        ("repetition_penalty", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+        ("presence_penalty", ctypes.c_float),
+        ("frequency_penalty", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+    ]
+
+
+class OrRowDiag(ctypes.Structure):
+    _fields_ = [
+        ("path", ctypes.c_uint32),
+        ("ranked", ctypes.c_uint32),
+        ("survivors", ctypes.c_uint32),
+        ("keep", ctypes.c_uint32),
+        ("keep_exact", ctypes.c_uint32),
+        ("pick", ctypes.c_uint32),
+        ("pick_exact", ctypes.c_uint32),
+        ("consumed_u", ctypes.c_uint32),
+        ("u_gap", ctypes.c_double),
+        ("p_gap", ctypes.c_double),
+        ("mass64", ctypes.c_double),
+        ("mass", ctypes.c_float),
+        ("best", ctypes.c_float),
+    ]
+
+
+DIAG_DTYPE = np.dtype(
+    [
+        ("path", "<u4"), ("ranked", "<u4"), ("survivors", "<u4"), ("keep", "<u4"),
+        ("keep_exact", "<u4"), ("pick", "<u4"), ("pick_exact", "<u4"),
+        ("consumed_u", "<u4"), ("u_gap", "<f8"), ("p_gap", "<f8"),
+        ("mass64", "<f8"), ("mass", "<f4"), ("best", "<f4"),
+    ],
+    align=True,
+)
+assert DIAG_DTYPE.itemsize == ctypes.sizeof(OrRowDiag)
+
+PATH_ARGMAX_FAST, PATH_TOP_N, PATH_CUTOFF, PATH_FALLBACK, PATH_NONE_ALLOWED = range(5)
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.or_rng_seed.restype = ctypes.c_uint64
+        L.or_rng_seed.argtypes = [ctypes.c_uint64]
+        L.or_rng_next.restype = ctypes.c_float
+        L.or_rng_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.or_top_n.restype = ctypes.c_size_t
+        L.or_top_n.argtypes = [c_f32p, ctypes.c_size_t, ctypes.c_size_t, c_f32p, c_u32p]
+        L.or_argmax.restype = ctypes.c_uint32
+        L.or_argmax.argtypes = [c_f32p, ctypes.c_size_t]
+        L.or_logprobs.restype = ctypes.c_float
+        L.or_logprobs.argtypes = [c_f32p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_size_t,
+                                  c_u32p, c_f32p, c_f32p]
+        L.or_penalize.restype = None
+        L.or_penalize.argtypes = [c_f32p, ctypes.c_size_t, c_u32p, ctypes.c_size_t,
+                                  ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        L.or_expf_array.restype = None
+        L.or_expf_array.argtypes = [c_f32p, c_f32p, ctypes.c_size_t]
+        L.or_sampler_new.restype = ctypes.c_void_p
+        L.or_sampler_new.argtypes = [ctypes.POINTER(OrConfig)]
+        L.or_sampler_free.restype = None
+        L.or_sampler_free.argtypes = [ctypes.c_void_p]
+        L.or_sampler_state.restype = ctypes.c_uint64
+        L.or_sampler_state.argtypes = [ctypes.c_void_p]
+        L.or_uniform.restype = ctypes.c_float
+        L.or_uniform.argtypes = [ctypes.c_void_p]
+        L.or_sample.restype = ctypes.c_uint32
+        L.or_sample.argtypes = [ctypes.c_void_p, c_f32p, ctypes.c_size_t, ctypes.c_size_t,
+                                c_u32p, ctypes.c_size_t]
+        L.or_sample_with.restype = ctypes.c_uint32
+        L.or_sample_with.argtypes = [ctypes.c_void_p, c_f32p, ctypes.c_size_t, ctypes.c_size_t,
+                                     c_u32p, ctypes.c_size_t, c_u32p]
+        L.or_distribution.restype = ctypes.c_size_t
+        L.or_distribution.argtypes = [ctypes.c_void_p, c_f32p, ctypes.c_size_t, ctypes.c_size_t,
+                                      c_u32p, ctypes.c_size_t, c_u32p, c_f32p, ctypes.c_size_t]
+        L.or_draw.restype = ctypes.c_uint32
+        L.or_draw.argtypes = [ctypes.c_void_p, c_u32p, c_f32p, ctypes.c_size_t]
+        L.or_verify.restype = ctypes.c_int
+        L.or_verify.argtypes = [c_u32p, c_f32p, ctypes.c_size_t, c_u32p, c_f32p, ctypes.c_size_t,
+                                ctypes.c_uint32, ctypes.c_float, c_u32p, c_f32p,
+                                ctypes.POINTER(ctypes.c_size_t)]
+        vp = ctypes.c_void_p
+        L.or_sample_batch.restype = ctypes.c_int
+        L.or_sample_batch.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp,
+                                      vp, vp, vp, ctypes.c_uint32, vp, vp, vp, vp, vp,
+                                      ctypes.c_uint32, vp, vp, vp, ctypes.c_int]
+        L.or_distribution_batch.restype = ctypes.c_int
+        L.or_distribution_batch.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                            vp, vp, vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int]
+        _lib = L
+    return _lib
+
+
+def _p(a, ct):
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+def _vp(a):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def top_n(x, n):
+    x = f32(x)
+    v = np.zeros(max(n, 1), np.float32)
+    i = np.zeros(max(n, 1), np.uint32)
+    k = lib().or_top_n(_p(x, ctypes.c_float), x.size, n, _p(v, ctypes.c_float), _p(i, ctypes.c_uint32))
+    return v[:k], i[:k]
+
+
+def argmax(x):
+    x = f32(x)
+    return int(lib().or_argmax(_p(x, ctypes.c_float), x.size))
+
+
+def logprobs(x, token, n):
+    x = f32(x)
+    ti = np.zeros(max(n, 1), np.uint32)
+    tl = np.zeros(max(n, 1), np.float32)
+    lse = ctypes.c_float()
+    lp = lib().or_logprobs(_p(x, ctypes.c_float), x.size, token, n, _p(ti, ctypes.c_uint32),
+                           _p(tl, ctypes.c_float), ctypes.byref(lse))
+    k = min(n, x.size)
+    return float(lp), ti[:k], tl[:k], float(lse.value)
+
+
+def penalize(x, recent, rep=1.0, pres=0.0, freq=0.0):
+    buf = f32(x).copy()
+    r = u32(recent)
+    lib().or_penalize(_p(buf, ctypes.c_float), buf.size, _p(r, ctypes.c_uint32), r.size, rep, pres, freq)
+    return buf
+
+
+def expf_array(x):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().or_expf_array(_p(x, ctypes.c_float), _p(y, ctypes.c_float), x.size)
+    return y
+
+
+class Sampler:
+    """The reference's Sampler object (sampler.rs:53-262) on the oracle."""
+
+    def __init__(self, temperature=0.7, top_k=20, top_p=0.8, repetition_penalty=1.05, seed=0,
+                 presence_penalty=0.0, frequency_penalty=0.0, min_p=0.0):
+        self.cfg = OrConfig(temperature, top_k, top_p, repetition_penalty, seed, presence_penalty,
+                            frequency_penalty, min_p)
+        self.h = lib().or_sampler_new(ctypes.byref(self.cfg))
+
+    @classmethod
+    def greedy(cls, **kw):
+        """SamplerConfig::greedy (sampler.rs:33-41)."""
+        base = dict(temperature=0.0, top_k=1, top_p=1.0, repetition_penalty=1.0, seed=0)
+        base.update(kw)
+        return cls(**base)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_sampler_free(self.h)
+            self.h = None
+
+    def sample(self, logits, vocab, recent=()):
+        x = f32(logits)
+        r = u32(list(recent) or [0])
+        return int(lib().or_sample(self.h, _p(x, ctypes.c_float), x.size, vocab, _p(r, ctypes.c_uint32),
+                                   len(recent)))
+
+    def sample_with(self, logits, vocab, recent, mask):
+        x = f32(logits)
+        r = u32(list(recent) or [0])
+        m = u32(mask)
+        return int(lib().or_sample_with(self.h, _p(x, ctypes.c_float), x.size, vocab,
+                                        _p(r, ctypes.c_uint32), len(recent), _p(m, ctypes.c_uint32)))
+
+    def distribution(self, logits, vocab, recent=()):
+        x = f32(logits)
+        r = u32(list(recent) or [0])
+        ids = np.zeros(x.size, np.uint32)
+        ps = np.zeros(x.size, np.float32)
+        k = lib().or_distribution(self.h, _p(x, ctypes.c_float), x.size, vocab, _p(r, ctypes.c_uint32),
+                                  len(recent), _p(ids, ctypes.c_uint32), _p(ps, ctypes.c_float), x.size)
+        return list(zip(ids[:k].tolist(), ps[:k].tolist()))
+
+    def draw(self, weighted):
+        ids = u32([t for t, _ in weighted] or [0])
+        w = f32([p for _, p in weighted] or [0])
+        return int(lib().or_draw(self.h, _p(ids, ctypes.c_uint32), _p(w, ctypes.c_float), len(weighted)))
+
+    def uniform(self):
+        return float(lib().or_uniform(self.h))
+
+    @property
+    def state(self):
+        return int(lib().or_sampler_state(self.h))
+
+
+def verify(p, q, x, u):
+    """speculative::verify (speculative.rs:167-189): ('accept', None) or
+    ('resample', residual)."""
+    pi = u32([t for t, _ in p] or [0])
+    pp = f32([v for _, v in p] or [0])
+    qi = u32([t for t, _ in q] or [0])
+    qp = f32([v for _, v in q] or [0])
+    ri = np.zeros(max(len(p), 1), np.uint32)
+    rp = np.zeros(max(len(p), 1), np.float32)
+    rn = ctypes.c_size_t()
+    acc = lib().or_verify(_p(pi, ctypes.c_uint32), _p(pp, ctypes.c_float), len(p), _p(qi, ctypes.c_uint32),
+                          _p(qp, ctypes.c_float), len(q), x, u, _p(ri, ctypes.c_uint32),
+                          _p(rp, ctypes.c_float), ctypes.byref(rn))
+    if acc:
+        return "accept", None
+    return "resample", list(zip(ri[: rn.value].tolist(), rp[: rn.value].tolist()))
+
+
+@dataclass
+class BatchResult:
+    token: np.ndarray
+    logprob: np.ndarray
+    top_ids: np.ndarray
+    top_lp: np.ndarray
+    prob: np.ndarray
+    keep: np.ndarray
+    diag: np.ndarray
+
+
+def sample_batch(w, nthreads=1) -> BatchResult:
+    """tsm_sample() on the oracle for a workload (tachyon_amd.workloads)."""
+    rows = w.rows
+    top_stride = max(1, w.top_stride)
+    token = np.zeros(rows, np.uint32)
+    logprob = np.zeros(rows, np.float32)
+    top_ids = np.zeros((rows, top_stride), np.uint32)
+    top_lp = np.zeros((rows, top_stride), np.float32)
+    prob = np.zeros(rows, np.float32)
+    keep = np.zeros(rows, np.uint32)
+    diag = np.zeros(rows, DIAG_DTYPE)
+    lib().or_sample_batch(
+        _vp(w.logits), rows, w.row_stride, w.usable, _vp(w.params), _vp(w.hist_ids),
+        _vp(w.hist_offsets), _vp(w.mask), w.mask_stride, _vp(w.uniforms), _vp(token),
+        _vp(logprob), _vp(top_ids), _vp(top_lp), top_stride, _vp(prob), _vp(keep), _vp(diag),
+        nthreads)
+    return BatchResult(token, logprob, top_ids, top_lp, prob, keep, diag)
+
+
+def distribution_batch(w, dist_stride, nthreads=1):
+    rows = w.rows
+    ids = np.zeros((rows, dist_stride), np.uint32)
+    ps = np.zeros((rows, dist_stride), np.float32)
+    keep = np.zeros(rows, np.uint32)
+    lib().or_distribution_batch(_vp(w.logits), rows, w.row_stride, w.usable, _vp(w.params),
+                                _vp(w.hist_ids), _vp(w.hist_offsets), _vp(ids), _vp(ps),
+                                dist_stride, _vp(keep), nthreads)
+    return ids, ps, keep

@@ -1,0 +1,278 @@
+"""Synthetic sampling workloads: the five BASELINE configurations and small
+random cases for parity tests.
+
+Each workload holds host (numpy) arrays laid out exactly as the C ABI
+expects (include/tachyon_sampler.h): logits [rows][row_stride] f32, per-row
+``tsm_row_params`` records, CSR history, packed LSB-first masks and one
+uniform per row.  Data is synthetic (there is no model here); its shapes and
+distributions follow the BASELINE config text.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+ROW_PARAMS_DTYPE = np.dtype(
+    [
+        ("temperature", "<f4"),
+        ("top_k", "<u4"),
+        ("top_p", "<f4"),
+        ("repetition_penalty", "<f4"),
+        ("presence_penalty", "<f4"),
+        ("frequency_penalty", "<f4"),
+        ("min_p", "<f4"),
+        ("flags", "<u4"),
+        ("n_logprobs", "<u4"),
+        ("reserved", "<u4"),
+    ]
+)
+assert ROW_PARAMS_DTYPE.itemsize == 40
+
+ROW_CONSTRAINED = 1
+ROW_LOGPROBS = 2
+
+QWEN_VOCAB = 151936
+LLAMA_VOCAB = 128256
+
+
+@dataclass
+class Workload:
+    name: str
+    logits: np.ndarray          # [rows, row_stride] f32
+    usable: int
+    params: np.ndarray          # [rows] ROW_PARAMS_DTYPE
+    hist_ids: np.ndarray | None
+    hist_offsets: np.ndarray | None
+    mask: np.ndarray | None     # [rows, mask_stride] u32
+    uniforms: np.ndarray        # [rows] f32
+    top_stride: int = 0
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def rows(self) -> int:
+        return int(self.logits.shape[0])
+
+    @property
+    def row_stride(self) -> int:
+        return int(self.logits.shape[1])
+
+    @property
+    def mask_stride(self) -> int:
+        return 0 if self.mask is None else int(self.mask.shape[1])
+
+    def algorithmic_bytes(self) -> int:
+        """Bytes one step must move at least: one read of every usable logit,
+        the mask words of constrained rows, the history ids and offsets, the
+        parameters and uniforms, and the outputs written."""
+        rows = self.rows
+        b = rows * self.usable * 4
+        if self.mask is not None:
+            nc = int(np.count_nonzero(self.params["flags"] & ROW_CONSTRAINED))
+            b += nc * ((self.usable + 31) // 32) * 4
+        if self.hist_ids is not None:
+            b += self.hist_ids.size * 4 + (rows + 1) * 4
+        b += rows * (ROW_PARAMS_DTYPE.itemsize + 4)          # params + uniform
+        nlp = self.params["n_logprobs"].astype(np.int64)
+        lp_rows = (self.params["flags"] & ROW_LOGPROBS) != 0
+        b += rows * 4 + int(np.sum(np.where(lp_rows, 4 + 8 * nlp, 0)))  # token, logprob, top
+        return int(b)
+
+
+def make_params(rows, temperature=0.7, top_k=0, top_p=1.0, repetition_penalty=1.0,
+                presence_penalty=0.0, frequency_penalty=0.0, min_p=0.0, flags=0, n_logprobs=0):
+    p = np.zeros(rows, ROW_PARAMS_DTYPE)
+    p["temperature"] = temperature
+    p["top_k"] = top_k
+    p["top_p"] = top_p
+    p["repetition_penalty"] = repetition_penalty
+    p["presence_penalty"] = presence_penalty
+    p["frequency_penalty"] = frequency_penalty
+    p["min_p"] = min_p
+    p["flags"] = flags
+    p["n_logprobs"] = n_logprobs
+    return p
+
+
+def uniforms(rng, rows):
+    """Per-row u = k / 2^24 with integer k, i.e. exactly the values
+    Sampler::next_f32 can produce (sampler.rs:260)."""
+    return (rng.integers(0, 1 << 24, size=rows).astype(np.float32) / np.float32(1 << 24)).astype(np.float32)
+
+
+def zipf_histories(rng, rows, length, vocab, a=1.1):
+    """Per-row histories of `length` ids whose ranks follow Zipf(a); rank -> id
+    through a seeded permutation of the vocabulary."""
+    perm = rng.permutation(vocab).astype(np.uint32)
+    ranks = np.empty((rows, length), np.int64)
+    filled = 0
+    flat = ranks.reshape(-1)
+    need = rows * length
+    while filled < need:
+        z = rng.zipf(a, size=2 * (need - filled))
+        z = z[z <= vocab]
+        take = min(z.size, need - filled)
+        flat[filled:filled + take] = z[:take]
+        filled += take
+    ids = perm[(ranks - 1) % vocab]
+    offsets = (np.arange(rows + 1, dtype=np.uint32) * length).astype(np.uint32)
+    return ids.reshape(-1).astype(np.uint32), offsets
+
+
+def uniform_histories(rng, rows, length, vocab):
+    ids = rng.integers(0, vocab, size=rows * length).astype(np.uint32)
+    offsets = (np.arange(rows + 1, dtype=np.uint32) * length).astype(np.uint32)
+    return ids, offsets
+
+
+def pack_mask(allowed: np.ndarray) -> np.ndarray:
+    """bool [rows, usable] -> u32 [rows, ceil(usable/32)], LSB-first."""
+    rows, n = allowed.shape
+    words = (n + 31) // 32
+    padded = np.zeros((rows, words * 32), bool)
+    padded[:, :n] = allowed
+    bits = padded.reshape(rows, words, 32).astype(np.uint64)
+    w = (bits << np.arange(32, dtype=np.uint64)).sum(axis=2)
+    return w.astype(np.uint32)
+
+
+def gaussian_logits(rng, rows, vocab, sigma):
+    x = rng.standard_normal((rows, vocab), dtype=np.float32)
+    x *= np.float32(sigma)
+    return x
+
+
+def c1(seed=0x5EED0001) -> Workload:
+    """B=1, V=151936, N(0,3^2) + 20 spikes of +8; T=.7 k=40 p=.9 R=1.1/64."""
+    rng = np.random.default_rng(seed)
+    V = QWEN_VOCAB
+    x = gaussian_logits(rng, 1, V, 3.0)
+    spikes = rng.choice(V, size=20, replace=False)
+    x[0, spikes] += np.float32(8.0)
+    ids, off = uniform_histories(rng, 1, 64, V)
+    p = make_params(1, temperature=0.7, top_k=40, top_p=0.9, repetition_penalty=1.1)
+    return Workload("c1", x, V, p, ids, off, None, uniforms(rng, 1))
+
+
+def c2(seed=0x5EED0002, rows=32) -> Workload:
+    """B=32 mixed rows (greedy / T=1 only / k=50 p=.95 / min_p=.05), N(0,2^2),
+    presence .5 frequency .3 over 512-token Zipf(1.1) histories."""
+    rng = np.random.default_rng(seed)
+    V = QWEN_VOCAB
+    x = gaussian_logits(rng, rows, V, 2.0)
+    ids, off = zipf_histories(rng, rows, 512, V)
+    p = make_params(rows, temperature=1.0, presence_penalty=0.5, frequency_penalty=0.3)
+    q = rows // 4
+    p["temperature"][:q] = 0.0
+    p["top_k"][2 * q:3 * q] = 50
+    p["top_p"][2 * q:3 * q] = 0.95
+    p["min_p"][3 * q:] = 0.05
+    return Workload("c2", x, V, p, ids, off, None, uniforms(rng, rows))
+
+
+def c3(seed=0x5EED0003, rows=256, vocab=LLAMA_VOCAB) -> Workload:
+    """B=256, V=128256, N(0,3^2); per-row mask with allowed fraction
+    log-uniform in [0.1%, 60%] (half contiguous ranges, half scattered);
+    T=.8 k=40 p=.9; top-20 logprobs."""
+    rng = np.random.default_rng(seed)
+    V = vocab
+    x = gaussian_logits(rng, rows, V, 3.0)
+    allowed = np.zeros((rows, V), bool)
+    for r in range(rows):
+        f = float(np.exp(rng.uniform(np.log(0.001), np.log(0.6))))
+        n_allow = max(1, int(round(f * V)))
+        if r % 2 == 0:
+            nr = int(rng.integers(1, 9))
+            lens = rng.multinomial(n_allow, np.ones(nr) / nr)
+            for ln in lens:
+                if ln == 0:
+                    continue
+                s = int(rng.integers(0, V - ln + 1))
+                allowed[r, s:s + ln] = True
+        else:
+            allowed[r, rng.choice(V, size=n_allow, replace=False)] = True
+    mask = pack_mask(allowed)
+    p = make_params(rows, temperature=0.8, top_k=40, top_p=0.9,
+                    flags=ROW_CONSTRAINED | ROW_LOGPROBS, n_logprobs=20)
+    return Workload("c3", x, V, p, None, None, mask, uniforms(rng, rows), top_stride=20)
+
+
+def c4(seed=0x5EED0004, rows=256) -> Workload:
+    """Headline: B=256, V=151936, N(0,3^2); R=1.1 + presence .4 + frequency .2
+    over 1024-token Zipf histories; 30% mask; T=.7 k=64 p=.92 min_p=.02;
+    top-5 logprobs."""
+    rng = np.random.default_rng(seed)
+    V = QWEN_VOCAB
+    x = gaussian_logits(rng, rows, V, 3.0)
+    ids, off = zipf_histories(rng, rows, 1024, V)
+    allowed = rng.random((rows, V), dtype=np.float32) < np.float32(0.3)
+    mask = pack_mask(allowed)
+    p = make_params(rows, temperature=0.7, top_k=64, top_p=0.92, min_p=0.02,
+                    repetition_penalty=1.1, presence_penalty=0.4, frequency_penalty=0.2,
+                    flags=ROW_CONSTRAINED | ROW_LOGPROBS, n_logprobs=5)
+    return Workload("c4", x, V, p, ids, off, mask, uniforms(rng, rows), top_stride=5)
+
+
+def c5(seed=0x5EED0005, rows=1024) -> Workload:
+    """Worst-case nucleus: B=1024, V=151936, N(0,1); T=1.2, no top-k,
+    p=.98, R=1.05 over 256-token histories."""
+    rng = np.random.default_rng(seed)
+    V = QWEN_VOCAB
+    x = gaussian_logits(rng, rows, V, 1.0)
+    ids, off = uniform_histories(rng, rows, 256, V)
+    p = make_params(rows, temperature=1.2, top_k=0, top_p=0.98, repetition_penalty=1.05)
+    return Workload("c5", x, V, p, ids, off, None, uniforms(rng, rows))
+
+
+CONFIGS = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5}
+
+
+def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, mask_frac=0.3,
+                logprobs=True, hist_len=16, penalties=True, mode="mixed", sigma=2.0):
+    """Small random workload for parity tests: mixed per-row settings, optional
+    heavy ties (integer-valued logits), masks and histories."""
+    rng = np.random.default_rng(seed)
+    stride = stride or vocab
+    if ties:
+        x = rng.integers(-4, 5, size=(rows, stride)).astype(np.float32)
+        x[rng.random((rows, stride)) < 0.05] = -0.0
+    else:
+        x = (rng.standard_normal((rows, stride)) * sigma).astype(np.float32)
+    p = make_params(rows)
+    for r in range(rows):
+        kind = mode if mode != "mixed" else ["greedy", "topk", "topp", "nucleus", "minp", "all"][r % 6]
+        t = float(rng.choice([0.0, 0.5, 0.7, 1.0, 1.3])) if kind != "greedy" else 0.0
+        if kind != "greedy" and t == 0.0:
+            t = 0.8
+        p["temperature"][r] = t
+        p["top_k"][r] = {"greedy": 1, "topk": int(rng.integers(1, 80)), "topp": int(rng.integers(1, 300)),
+                         "nucleus": 0, "minp": 0, "all": int(rng.integers(0, 200))}[kind]
+        p["top_p"][r] = {"greedy": 1.0, "topk": 1.0, "topp": float(rng.uniform(0.3, 0.99)),
+                         "nucleus": float(rng.uniform(0.5, 1.0)), "minp": 1.0,
+                         "all": float(rng.uniform(0.5, 0.99))}[kind]
+        p["min_p"][r] = {"minp": float(rng.uniform(0.01, 0.5)), "all": float(rng.uniform(0.0, 0.1))}.get(kind, 0.0)
+        if penalties:
+            p["repetition_penalty"][r] = float(rng.choice([1.0, 1.1, 0.9, 2.0]))
+            p["presence_penalty"][r] = float(rng.choice([0.0, 0.4, -0.3]))
+            p["frequency_penalty"][r] = float(rng.choice([0.0, 0.2, 0.5]))
+        flags = 0
+        if masked and rng.random() < 0.8:
+            flags |= ROW_CONSTRAINED
+        if logprobs and rng.random() < 0.7:
+            flags |= ROW_LOGPROBS
+            p["n_logprobs"][r] = int(rng.integers(0, 21))
+        p["flags"][r] = flags
+    if hist_len > 0:
+        lens = rng.integers(0, hist_len + 1, size=rows)
+        offs = np.zeros(rows + 1, np.uint32)
+        offs[1:] = np.cumsum(lens)
+        ids = rng.integers(0, vocab + 3, size=int(offs[-1])).astype(np.uint32)  # a few ids >= usable
+    else:
+        ids, offs = None, None
+    mask = None
+    if masked:
+        fr = rng.uniform(0.0, mask_frac, size=(rows, 1))
+        allowed = rng.random((rows, vocab)) < fr
+        mask = pack_mask(allowed)
+    top_stride = 20 if logprobs else 0
+    return Workload(f"rand{seed}", x, vocab, p, ids, offs, mask, uniforms(rng, rows), top_stride=top_stride)

@@ -1,0 +1,312 @@
+"""Pins the CPU oracle (oracle/tachyon_oracle.cpp) before it is trusted as
+the parity checker of the GPU path.
+
+* The reference's own known-answer tests, ported from
+  /root/reference/src/sampler.rs:328-395 and src/speculative.rs:349-391.
+* Closed forms and hand-derived expectations (penalties, log-softmax).
+* A mathematical pin of the RNG: the xorshift triple (12, 25, 27) gives a
+  full-period generator over GF(2)^64.
+* Brute force against oracle/naive.py, an independent full-sort restatement,
+  on small and tie-heavy random inputs covering every row kind.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import naive
+from tachyon_amd import workloads as wl
+
+
+# --------------------------------------------------------------------------
+# sampler.rs:328-395, ported
+# --------------------------------------------------------------------------
+
+def test_reference_greedy_and_top_k(oracle):
+    logits = [0.1, 3.0, 2.9, -1.0]
+    assert oracle.Sampler.greedy().sample(logits, 4) == 1
+    s = oracle.Sampler(temperature=1.0, top_k=2, top_p=1.0, repetition_penalty=1.0, seed=3)
+    for _ in range(200):
+        assert s.sample(logits, 4) in (1, 2)
+
+
+def test_reference_constraint_and_distribution(oracle):
+    logits = [0.1, 3.0, 2.9, -1.0]
+    s = oracle.Sampler.greedy()
+    allowed = np.array([True, False, True, True])  # |t| t != 1
+    mask = wl.pack_mask(allowed[None, :])[0]
+    assert s.sample_with(logits, 4, [], mask) == 2
+    s = oracle.Sampler(temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0, seed=1)
+    d = s.distribution(logits, 4)
+    assert d[0][0] == 1
+    assert abs(np.float32(sum(np.float32(p) for _, p in d)) - 1.0) < 1e-5
+
+
+def test_reference_top_n_matches_a_full_sort(oracle):
+    x = np.array([((i * 2654435761) & 0xFFFFFFFF) % 10007 for i in range(5000)], np.float32)
+    srt = sorted(((float(v), i) for i, v in enumerate(x)), key=lambda t: -t[0])
+    vals, _ = oracle.top_n(x, 37)
+    assert vals.tolist() == [v for v, _ in srt[:37]]
+
+
+def test_reference_logprobs_are_log_softmax(oracle):
+    lp, top_ids, _, _ = oracle.logprobs([1.0, 2.0, 3.0], 1, 2)
+    f = np.float32
+    z = f(math.log(float(f(math.exp(1.0)) + f(math.exp(2.0)) + f(math.exp(3.0)))))
+    assert abs(lp - (2.0 - z)) < 1e-5
+    assert top_ids.tolist() == [2, 1]
+
+
+def test_reference_penalty_can_flip_the_choice(oracle):
+    s = oracle.Sampler.greedy(repetition_penalty=2.0)
+    assert s.sample([0.0, 3.0, 2.0], 3, [1]) == 2
+
+
+# --------------------------------------------------------------------------
+# speculative.rs:349-391, ported (draw / uniform / verify)
+# --------------------------------------------------------------------------
+
+def test_reference_speculative_sampling_preserves_the_target_distribution(oracle):
+    p = [(0, 0.5), (1, 0.3), (2, 0.2)]
+    q = [(0, 0.2), (1, 0.6), (2, 0.2)]
+    rng = oracle.Sampler(temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0, seed=7)
+    trials = 200_000
+    counts = [0, 0, 0]
+    for _ in range(trials):
+        x = rng.draw(q)
+        u = rng.uniform()
+        verdict, residual = oracle.verify(p, q, x, u)
+        t = x if verdict == "accept" else rng.draw(residual)
+        counts[t] += 1
+    for i, (_, want) in enumerate(p):
+        assert abs(counts[i] / trials - want) < 0.01
+
+
+def test_reference_deterministic_drafts_reduce_to_greedy(oracle):
+    p = [(4, 1.0)]
+    assert oracle.verify(p, [], 4, 0.99)[0] == "accept"
+    v, r = oracle.verify(p, [], 5, 0.0)
+    assert v == "resample" and r == [(4, 1.0)]
+
+
+# --------------------------------------------------------------------------
+# RNG (sampler.rs:64, :255-261)
+# --------------------------------------------------------------------------
+
+def _gf2_step_matrix(a, b, c):
+    """Columns of the GF(2) matrix of x ^= x>>a; x ^= x<<b; x ^= x>>c."""
+    M64 = (1 << 64) - 1
+
+    def step(x):
+        x ^= x >> a
+        x ^= (x << b) & M64
+        x ^= x >> c
+        return x
+
+    return [step(1 << i) for i in range(64)]
+
+
+def _gf2_mul(A, B):
+    # (A*B) column j = A applied to column j of B
+    out = []
+    for col in B:
+        v = 0
+        i = 0
+        while col:
+            if col & 1:
+                v ^= A[i]
+            col >>= 1
+            i += 1
+        out.append(v)
+    return out
+
+
+def _gf2_pow(A, e):
+    R = [1 << i for i in range(64)]
+    while e:
+        if e & 1:
+            R = _gf2_mul(A, R)
+        A = _gf2_mul(A, A)
+        e >>= 1
+    return R
+
+
+def test_rng_xorshift_triple_has_full_period():
+    """(12, 25, 27) must make the state map a full-period linear map: order
+    exactly 2^64-1.  A wrong shift or direction breaks this."""
+    M = _gf2_step_matrix(12, 25, 27)
+    ident = [1 << i for i in range(64)]
+    n = (1 << 64) - 1
+    assert _gf2_pow(M, n) == ident
+    for q in (3, 5, 17, 257, 641, 65537, 6700417):
+        assert _gf2_pow(M, n // q) != ident
+    # a plausible typo is not full period
+    assert _gf2_pow(_gf2_step_matrix(12, 25, 26), n) != ident
+
+
+def test_rng_two_restatements_agree_and_output_grid(oracle):
+    assert 0x2545F4914F6CDD1D == 2685821657736338717  # xorshift64* multiplier (Vigna)
+    for seed in (0, 1, 3, 7, 0xDEADBEEF, (1 << 64) - 1):
+        s = oracle.Sampler(seed=seed)
+        st = naive.rng_seed(seed)
+        assert s.state == st
+        for _ in range(500):
+            u, st = naive.rng_next(st)
+            v = s.uniform()
+            assert v == u
+            assert 0.0 <= v < 1.0 and float(v * (1 << 24)).is_integer()
+    # uniformity of the output over 2^18 draws (mean and a 64-bin chi-square)
+    s = oracle.Sampler(seed=12345)
+    us = np.array([s.uniform() for _ in range(1 << 18)])
+    assert abs(us.mean() - 0.5) < 3e-3
+    h, _ = np.histogram(us, bins=64, range=(0, 1))
+    chi2 = float(((h - h.mean()) ** 2 / h.mean()).sum())
+    assert chi2 < 120  # 63 dof; p ~ 1e-5 bound
+
+
+# --------------------------------------------------------------------------
+# Closed forms
+# --------------------------------------------------------------------------
+
+def test_penalties_hand_derived(oracle):
+    x = np.array([2.0, -2.0, 0.0, -0.0, 5.0], np.float32)
+    got = oracle.penalize(x, [0, 1, 2, 3, 3, 9], rep=2.0, pres=0.5, freq=0.25)
+    # id0: 2/2=1 -> (1-.25)-.5 ; id1: -2*2=-4 -> (-4-.25)-.5 ; id2: 0 is not >0 -> 0*2=0 -> (0-.25)-.5
+    # id3 (count 2): -0*2=-0 -> (-0-.5)-.5 ; id4 untouched ; id9 >= n ignored
+    assert got.tolist() == [0.25, -4.75, -0.75, -1.0, 5.0]
+    # repetition only: count-insensitive (sampler.rs:166-168 dedups)
+    got = oracle.penalize(x, [0, 0, 0, 1], rep=2.0)
+    assert got.tolist() == [1.0, -4.0, 0.0, -0.0, 5.0]
+
+
+def test_logprobs_closed_form(oracle):
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        x = (rng.standard_normal(3000) * 3).astype(np.float32)
+        tok = int(rng.integers(0, 3000))
+        lp, ids, lps, lse = oracle.logprobs(x, tok, 7)
+        exact = float(x.max()) + math.log(math.fsum(math.exp(float(v) - float(x.max())) for v in x))
+        assert abs(lse - exact) < 2e-6
+        assert abs(lp - (float(x[tok]) - exact)) < 4e-6
+        order = np.lexsort((np.arange(3000), -x.astype(np.float64)))[:7]
+        assert ids.tolist() == order.tolist()
+
+
+def test_argmax_first_maximum_and_zeros(oracle):
+    assert oracle.argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert oracle.argmax([-0.0, 0.0, -1.0]) == 0  # -0 == +0: first wins
+    assert oracle.argmax([-np.inf, -np.inf]) == 0
+
+
+def test_top_n_matches_full_sort_with_ties(oracle):
+    rng = np.random.default_rng(11)
+    for _ in range(30):
+        n = int(rng.integers(1, 400))
+        x = rng.integers(-3, 4, size=n).astype(np.float32)
+        x[rng.random(n) < 0.1] = -0.0
+        k = int(rng.integers(0, n + 5))
+        vals, ids = oracle.top_n(x, k)
+        ref = naive.ieee_rank(x)[:k]
+        assert ids.tolist() == ref
+
+
+# --------------------------------------------------------------------------
+# Brute force: C++ oracle vs the naive full-sort restatement
+# --------------------------------------------------------------------------
+
+def _naive_batch(w):
+    out = []
+    for r in range(w.rows):
+        p = w.params[r]
+        if w.hist_offsets is not None:
+            rec = w.hist_ids[w.hist_offsets[r]:w.hist_offsets[r + 1]]
+        else:
+            rec = []
+        constrained = bool(p["flags"] & wl.ROW_CONSTRAINED)
+        tok, keep, prob = naive.sample_row(
+            w.logits[r, :w.usable], p["temperature"], int(p["top_k"]), p["top_p"],
+            p["repetition_penalty"], rec, w.mask[r] if constrained else None, w.uniforms[r],
+            p["presence_penalty"], p["frequency_penalty"], p["min_p"], constrained)
+        lp = None
+        if p["flags"] & wl.ROW_LOGPROBS:
+            lp = naive.logprobs(w.logits[r, :w.usable], tok, int(p["n_logprobs"]))
+        out.append((tok, keep, prob, lp))
+    return out
+
+
+CASES = [
+    dict(seed=1, vocab=300),
+    dict(seed=2, vocab=300, ties=True),
+    dict(seed=3, vocab=300, masked=True),
+    dict(seed=4, vocab=300, masked=True, ties=True, mask_frac=0.05),
+    dict(seed=5, vocab=1500, masked=True, mask_frac=0.02, rows=12),
+    dict(seed=6, vocab=2100, rows=12, mode="nucleus"),
+    dict(seed=7, vocab=2100, rows=12, mode="minp", ties=True),
+    dict(seed=8, vocab=64, rows=12, stride=80, masked=True, ties=True),
+    dict(seed=9, vocab=1200, rows=12, mode="topp", sigma=8.0),
+    dict(seed=10, vocab=5, rows=12, masked=True, mask_frac=0.6),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"s{c['seed']}" for c in CASES])
+def test_oracle_matches_naive(oracle, case):
+    w = wl.random_case(**case)
+    got = oracle.sample_batch(w)
+    ref = _naive_batch(w)
+    for r, (tok, keep, prob, lp) in enumerate(ref):
+        assert int(got.token[r]) == tok, (r, w.params[r])
+        assert int(got.keep[r]) == keep, r
+        assert struct.pack("<f", got.prob[r]) == struct.pack("<f", np.float32(prob)), r
+        if lp is not None:
+            assert struct.pack("<f", got.logprob[r]) == struct.pack("<f", np.float32(lp[0])), r
+            n = len(lp[1])
+            assert got.top_ids[r, :n].tolist() == [i for i, _ in lp[1]]
+            assert np.array_equal(got.top_lp[r, :n], np.array([v for _, v in lp[1]], np.float32))
+
+
+def test_oracle_edge_cases(oracle):
+    V = 40
+    x = np.linspace(-2, 2, V).astype(np.float32)[None, :]
+    base = dict(logits=x, usable=V, hist_ids=None, hist_offsets=None, uniforms=np.array([0.5], np.float32))
+
+    def run(params, mask=None):
+        w = wl.Workload("edge", params=params, mask=mask, **base)
+        return oracle.sample_batch(w)
+
+    # k > V behaves as k = V
+    a = run(wl.make_params(1, temperature=1.0, top_k=1000))
+    b = run(wl.make_params(1, temperature=1.0, top_k=V))
+    assert a.token[0] == b.token[0]
+    # nothing allowed -> argmax of the raw row, keep 0, no uniform consumed
+    m = wl.pack_mask(np.zeros((1, V), bool))
+    r = run(wl.make_params(1, temperature=1.0, top_k=5, flags=wl.ROW_CONSTRAINED), m)
+    assert r.token[0] == V - 1 and r.keep[0] == 0 and r.diag["consumed_u"][0] == 0
+    # only low ids allowed: outside the 256-window is impossible here (V < 256),
+    # so window = V and the best allowed wins greedily
+    allowed = np.zeros((1, V), bool)
+    allowed[0, :3] = True
+    r = run(wl.make_params(1, temperature=0.0, flags=wl.ROW_CONSTRAINED), wl.pack_mask(allowed))
+    assert r.token[0] == 2
+    # min_p keeps at least the best candidate
+    r = run(wl.make_params(1, temperature=1.0, min_p=1.0))
+    assert r.token[0] == V - 1 and r.keep[0] == 1
+
+
+def test_constrained_window_rule_differs_from_mask_then_topk(oracle):
+    """sampler.rs:184-222: rank the 256-wide window of UNMASKED logits, drop
+    disallowed ids, then truncate to k.  With 0 < allowed-in-window < k the
+    kept set is smaller than mask-then-top-k would give."""
+    V = 1000
+    x = np.arange(V, dtype=np.float32)[::-1].copy()[None, :] / 10  # id 0 best
+    allowed = np.zeros((1, V), bool)
+    allowed[0, [5, 600, 601, 602]] = True  # one inside the top-256 window
+    w = wl.Workload("win", x, V, wl.make_params(1, temperature=1.0, top_k=3, flags=wl.ROW_CONSTRAINED),
+                    None, None, wl.pack_mask(allowed), np.array([0.99], np.float32))
+    r = oracle.sample_batch(w)
+    assert r.token[0] == 5 and r.keep[0] == 1
+    # nothing allowed inside the window -> whole-vocabulary fallback, then top-3
+    allowed[0, 5] = False
+    w.mask = wl.pack_mask(allowed)
+    r = oracle.sample_batch(w)
+    assert r.diag["path"][0] == 3 and r.keep[0] == 3 and r.token[0] in (600, 601, 602)
