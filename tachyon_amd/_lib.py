@@ -1,0 +1,87 @@
+"""ctypes binding of the HIP sampling library (lib/libtachyon_sampler.so).
+
+This is the product path: every call goes to the gfx950 kernels through the C
+ABI of include/tachyon_sampler.h.  There is no CPU fallback; if the library
+is missing, loading fails with an error that says how to build it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtachyon_sampler.so")
+
+vp = ctypes.c_void_p
+u32 = ctypes.c_uint32
+
+
+class TsmBatch(ctypes.Structure):
+    _fields_ = [
+        ("logits", vp),
+        ("rows", u32),
+        ("row_stride", u32),
+        ("usable", u32),
+        ("mask_stride", u32),
+        ("params", vp),
+        ("hist_ids", vp),
+        ("hist_offsets", vp),
+        ("mask", vp),
+        ("uniforms", vp),
+    ]
+
+
+class TsmOutputs(ctypes.Structure):
+    _fields_ = [
+        ("token", vp),
+        ("logprob", vp),
+        ("top_ids", vp),
+        ("top_logprobs", vp),
+        ("top_stride", u32),
+        ("reserved", u32),
+        ("prob", vp),
+        ("keep", vp),
+    ]
+
+
+SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version"]
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python tachyon_amd/build.py`")
+        L = ctypes.CDLL(LIB_PATH)
+        L.tsm_create.restype = vp
+        L.tsm_create.argtypes = [ctypes.c_int, u32, u32, ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_destroy.restype = None
+        L.tsm_destroy.argtypes = [vp]
+        L.tsm_sample.restype = ctypes.c_int
+        L.tsm_sample.argtypes = [vp, vp, ctypes.POINTER(TsmBatch), ctypes.POINTER(TsmOutputs),
+                                 ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_distribution.restype = ctypes.c_int
+        L.tsm_distribution.argtypes = [vp, vp, ctypes.POINTER(TsmBatch), vp, vp, u32, vp,
+                                       ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_status.restype = ctypes.c_int
+        L.tsm_status.argtypes = [vp, ctypes.POINTER(u32), ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_version.restype = ctypes.c_char_p
+        L.tsm_version.argtypes = []
+        _lib = L
+    return _lib
+
+
+class TsmError(RuntimeError):
+    pass
+
+
+def _err():
+    return ctypes.create_string_buffer(1024)

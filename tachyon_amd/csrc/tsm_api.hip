@@ -1,0 +1,231 @@
+// tsm_api.hip - the C ABI (include/tachyon_sampler.h): context, argument
+// checks on the host, and the two launches of a step on the caller's stream.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "tsm_launch.h"
+
+struct tsm_ctx {
+    int device;
+    uint32_t max_rows, max_vocab, max_chunks;
+    tsm::ChunkStats* stats;
+    uint2* cand;
+    uint2* pen;
+    uint2* allow;
+    uint32_t* status;
+};
+
+namespace {
+
+void set_err(char* err, size_t errlen, const char* fmt, ...) {
+    if (!err || errlen == 0) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_batch(const tsm_ctx* ctx, const tsm_batch* b, char* err, size_t errlen) {
+    if (!ctx) return set_err(err, errlen, "context is NULL"), 1;
+    if (!b) return set_err(err, errlen, "batch is NULL"), 1;
+    if (!b->logits) return set_err(err, errlen, "batch->logits is NULL"), 1;
+    if (!b->params) return set_err(err, errlen, "batch->params is NULL"), 1;
+    if (b->rows == 0) return set_err(err, errlen, "batch->rows is 0"), 1;
+    if (b->rows > ctx->max_rows)
+        return set_err(err, errlen, "batch->rows %u exceeds the context's max_rows %u", b->rows, ctx->max_rows), 1;
+    if (b->usable == 0) return set_err(err, errlen, "batch->usable is 0"), 1;
+    if (b->usable > ctx->max_vocab)
+        return set_err(err, errlen, "batch->usable %u exceeds the context's max_vocab %u", b->usable, ctx->max_vocab), 1;
+    if (b->usable > b->row_stride)
+        return set_err(err, errlen, "batch->usable %u exceeds row_stride %u", b->usable, b->row_stride), 1;
+    if ((b->hist_ids == nullptr) != (b->hist_offsets == nullptr))
+        return set_err(err, errlen, "hist_ids and hist_offsets must both be set or both be NULL"), 1;
+    if (b->mask && b->mask_stride < (b->usable + 31) / 32)
+        return set_err(err, errlen, "mask_stride %u is below ceil(usable/32) = %u", b->mask_stride,
+                       (b->usable + 31) / 32), 1;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tsm_version(void) { return "tachyon-sampler 0.1 gfx950"; }
+
+tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err, size_t errlen) {
+    if (max_rows == 0 || max_rows > 65535) {
+        set_err(err, errlen, "max_rows must be in [1, 65535], got %u", max_rows);
+        return nullptr;
+    }
+    if (max_vocab == 0 || max_vocab > TSM_MAX_VOCAB) {
+        set_err(err, errlen, "max_vocab must be in [1, %u], got %u", TSM_MAX_VOCAB, max_vocab);
+        return nullptr;
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        set_err(err, errlen, "HIP device %d not available (%d devices)", device, ndev);
+        return nullptr;
+    }
+    DeviceGuard g(device);
+    if (!g.ok) {
+        set_err(err, errlen, "hipSetDevice(%d) failed", device);
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        set_err(err, errlen, "hipGetDeviceProperties failed");
+        return nullptr;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_err(err, errlen, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+        return nullptr;
+    }
+    tsm_ctx* c = new tsm_ctx();
+    c->device = device;
+    c->max_rows = max_rows;
+    c->max_vocab = max_vocab;
+    c->max_chunks = (max_vocab + tsm::kChunk - 1) / tsm::kChunk;
+    const size_t slots = static_cast<size_t>(max_rows) * c->max_chunks;
+    hipError_t e = hipSuccess;
+    e = hipMalloc(&c->stats, slots * sizeof(tsm::ChunkStats));
+    if (e == hipSuccess) e = hipMalloc(&c->cand, slots * tsm::kCandCap * sizeof(uint2));
+    if (e == hipSuccess) e = hipMalloc(&c->pen, slots * tsm::kPenCap * sizeof(uint2));
+    if (e == hipSuccess) e = hipMalloc(&c->allow, slots * tsm::kAllowCap * sizeof(uint2));
+    if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
+    if (e == hipSuccess) {
+        e = tsm::finalize_set_smem_attr();
+    }
+    if (e != hipSuccess) {
+        set_err(err, errlen, "device allocation failed: %s", hipGetErrorString(e));
+        tsm_destroy(c);
+        return nullptr;
+    }
+    return c;
+}
+
+void tsm_destroy(tsm_ctx* ctx) {
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    (void)hipDeviceSynchronize();
+    if (ctx->stats) (void)hipFree(ctx->stats);
+    if (ctx->cand) (void)hipFree(ctx->cand);
+    if (ctx->pen) (void)hipFree(ctx->pen);
+    if (ctx->allow) (void)hipFree(ctx->allow);
+    if (ctx->status) (void)hipFree(ctx->status);
+    delete ctx;
+}
+
+static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs* out, uint32_t* dist_ids,
+               float* dist_probs, uint32_t dist_stride, uint32_t* keep, bool distribution, char* err,
+               size_t errlen) {
+    if (check_batch(ctx, b, err, errlen)) return 1;
+    DeviceGuard g(ctx->device);
+    if (!g.ok) return set_err(err, errlen, "hipSetDevice(%d) failed", ctx->device), 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t n_chunks = (b->usable + tsm::kChunk - 1) / tsm::kChunk;
+    const bool vec = (b->row_stride % 4 == 0) && aligned16(b->logits);
+
+    tsm::SweepArgs sa;
+    sa.logits = b->logits;
+    sa.params = b->params;
+    sa.hist_ids = b->hist_ids;
+    sa.hist_off = b->hist_offsets;
+    sa.mask = distribution ? nullptr : b->mask;
+    sa.stats = ctx->stats;
+    sa.cand = ctx->cand;
+    sa.pen = ctx->pen;
+    sa.allow = ctx->allow;
+    sa.status = ctx->status;
+    sa.row_stride = b->row_stride;
+    sa.usable = b->usable;
+    sa.mask_stride = b->mask_stride;
+    sa.n_chunks = n_chunks;
+
+    tsm::FinArgs fa;
+    std::memset(&fa, 0, sizeof(fa));
+    fa.logits = b->logits;
+    fa.params = b->params;
+    fa.hist_ids = b->hist_ids;
+    fa.hist_off = b->hist_offsets;
+    fa.mask = sa.mask;
+    fa.uniforms = b->uniforms;
+    fa.stats = ctx->stats;
+    fa.cand = ctx->cand;
+    fa.pen = ctx->pen;
+    fa.allow = ctx->allow;
+    fa.status = ctx->status;
+    fa.row_stride = b->row_stride;
+    fa.usable = b->usable;
+    fa.mask_stride = b->mask_stride;
+    fa.n_chunks = n_chunks;
+    fa.distribution = distribution ? 1u : 0u;
+    if (distribution) {
+        fa.dist_ids = dist_ids;
+        fa.dist_probs = dist_probs;
+        fa.dist_stride = dist_stride;
+        fa.out_keep = keep;
+    } else {
+        fa.out_token = out->token;
+        fa.out_logprob = out->logprob;
+        fa.out_top_ids = out->top_ids;
+        fa.out_top_lp = out->top_logprobs;
+        fa.top_stride = out->top_stride;
+        fa.out_prob = out->prob;
+        fa.out_keep = out->keep;
+    }
+    tsm::launch_sweep(sa, b->rows, vec, s);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(err, errlen, "sweep launch failed: %s", hipGetErrorString(e)), 1;
+    tsm::launch_finalize(fa, b->rows, s);
+    e = hipGetLastError();
+    if (e != hipSuccess) return set_err(err, errlen, "finalize launch failed: %s", hipGetErrorString(e)), 1;
+    return 0;
+}
+
+int tsm_sample(tsm_ctx* ctx, void* stream, const tsm_batch* batch, const tsm_outputs* out, char* err,
+               size_t errlen) {
+    if (!out || !out->token) return set_err(err, errlen, "outputs->token is NULL"), 1;
+    if (batch && !batch->uniforms) return set_err(err, errlen, "batch->uniforms is NULL"), 1;
+    if ((out->top_ids || out->top_logprobs) && out->top_stride == 0)
+        return set_err(err, errlen, "top_stride is 0 while top_ids/top_logprobs are given"), 1;
+    if (out->top_logprobs && !out->top_ids)
+        return set_err(err, errlen, "top_logprobs needs top_ids"), 1;
+    if (out->top_stride > TSM_MAX_LOGPROBS && (out->top_ids || out->top_logprobs))
+        return set_err(err, errlen, "top_stride %u exceeds TSM_MAX_LOGPROBS", out->top_stride), 1;
+    return run(ctx, stream, batch, out, nullptr, nullptr, 0, nullptr, false, err, errlen);
+}
+
+int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch, uint32_t* dist_ids, float* dist_probs,
+                     uint32_t dist_stride, uint32_t* keep, char* err, size_t errlen) {
+    if (!dist_ids || !dist_probs || !keep) return set_err(err, errlen, "dist_ids, dist_probs and keep are required"), 1;
+    if (dist_stride == 0) return set_err(err, errlen, "dist_stride is 0"), 1;
+    return run(ctx, stream, batch, nullptr, dist_ids, dist_probs, dist_stride, keep, true, err, errlen);
+}
+
+int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen) {
+    if (!ctx || !status) return set_err(err, errlen, "context or status is NULL"), 1;
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(status, ctx->status, sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemset(ctx->status, 0, sizeof(uint32_t));
+    if (e != hipSuccess) return set_err(err, errlen, "status read failed: %s", hipGetErrorString(e)), 1;
+    return 0;
+}
+
+}  // extern "C"

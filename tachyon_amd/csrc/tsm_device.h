@@ -1,0 +1,275 @@
+// tsm_device.h - constants, scratch records and device helpers shared by the
+// sampling kernels (gfx950, wave64).  Compiled with -ffp-contract=off: every
+// float/double operation below rounds on its own unless an fma is written out.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tachyon_sampler.h"
+
+namespace tsm {
+
+// ---- geometry --------------------------------------------------------------
+constexpr int kWave = 64;
+constexpr int kSweepThreads = 256;                        // 4 waves
+constexpr int kSweepVec = 16;                             // float4 per thread
+constexpr uint32_t kChunk = kSweepThreads * kSweepVec * 4;  // 16384 ids per chunk
+constexpr int kGroupVec = 2;                              // float4 per group
+constexpr int kGroups = kSweepVec / kGroupVec;            // 8 groups of 8 per thread
+constexpr uint32_t kCandCap = 2048;    // candidate slots per chunk
+constexpr uint32_t kPenCap = 1024;     // penalized-id slots per chunk
+constexpr uint32_t kAllowCap = 1024;   // allowed-id slots per chunk (sparse masks)
+constexpr uint32_t kMaxWindow = 1024;  // top_n path bound (sampler.rs:193)
+constexpr uint32_t kWideWindow = 256;  // constrained window floor (sampler.rs:186-187)
+constexpr int kFinThreads = 1024;      // 16 waves
+constexpr uint32_t kMergeCap = 4096;   // candidates merged in LDS
+constexpr uint32_t kExactCap = 1024;   // longest list the exact path sorts
+constexpr uint32_t kTile = 16384;      // ids per tile of a re-read pass
+constexpr uint32_t kBins = 2048;       // radix histogram bins (11-bit digits)
+
+// ---- scratch records -------------------------------------------------------
+enum : uint32_t {
+    CS_HAS_CAND = 1u,       // the chunk wrote candidates
+    CS_CAND_OVERFLOW = 2u,  // more candidates than kCandCap (or Wc > cap)
+    CS_PEN_OVERFLOW = 4u,   // more penalized ids than kPenCap
+    CS_ALLOW_LIST = 8u,     // every allowed id of the chunk is in its list
+};
+
+struct ChunkStats {         // 32 bytes, one per (row, chunk)
+    double raw_sum;         // sum over the chunk of exp(x - raw_max)
+    float raw_max;          // max raw logit of the chunk
+    uint32_t n_cand;        // candidates found (may exceed kCandCap)
+    uint32_t n_pen;         // distinct history ids inside the chunk
+    uint32_t n_allowed;     // mask popcount over the chunk
+    uint32_t flags;         // CS_*
+    uint32_t pad;
+};
+static_assert(sizeof(ChunkStats) == 32, "ChunkStats layout");
+
+// ---- per-row mode (sampler.rs:161-190 + extensions) -------------------------
+struct RowMode {
+    float t;                // temperature, 1 when greedy
+    uint32_t want;          // kept after truncation (A3)
+    uint32_t window;        // ranked before the mask filter (A3)
+    uint32_t nlp;           // logprob alternatives
+    bool greedy, topk, constrained, logprobs, pen_rep, pen_pf, penal;
+};
+
+__device__ __host__ inline RowMode row_mode(const tsm_row_params& p, uint32_t n,
+                                            uint32_t hist_len, bool have_mask) {
+    RowMode m;
+    m.greedy = p.temperature <= 0.0f;
+    m.t = m.greedy ? 1.0f : p.temperature;
+    m.want = m.greedy ? 1u : (p.top_k == 0 ? n : (p.top_k < n ? p.top_k : n));
+    m.constrained = have_mask && (p.flags & TSM_ROW_CONSTRAINED);
+    uint32_t w = m.want > kWideWindow ? m.want : kWideWindow;
+    m.window = m.constrained ? (w < n ? w : n) : m.want;
+    m.topk = m.window <= kMaxWindow;
+    m.logprobs = (p.flags & TSM_ROW_LOGPROBS) != 0;
+    uint32_t nl = p.n_logprobs < TSM_MAX_LOGPROBS ? p.n_logprobs : TSM_MAX_LOGPROBS;
+    m.nlp = m.logprobs ? (nl < n ? nl : n) : 0u;
+    m.pen_rep = hist_len > 0 && p.repetition_penalty != 1.0f;
+    m.pen_pf = hist_len > 0 && (p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f);
+    m.penal = m.pen_rep || m.pen_pf;
+    return m;
+}
+
+// Repetition penalty (sampler.rs:172) then presence/frequency (extension),
+// for an id that occurs `c` > 0 times in the row's history.
+__device__ __forceinline__ float penalize(float l, uint32_t c, const RowMode& m,
+                                          const tsm_row_params& p) {
+    if (m.pen_rep) l = l > 0.0f ? l / p.repetition_penalty : l * p.repetition_penalty;
+    if (m.pen_pf) {
+        float fc = p.frequency_penalty * static_cast<float>(c);
+        l = l - fc;
+        l = l - p.presence_penalty;
+    }
+    return l;
+}
+
+// ---- order keys ---------------------------------------------------------------
+// f32::total_cmp order as an unsigned key (sort_unstable_by, sampler.rs:207).
+__device__ __forceinline__ uint32_t total_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// IEEE order with -0 == +0, as top_n's >= / > compare (sampler.rs:274-275).
+__device__ __forceinline__ uint32_t canon_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u << 1) == 0) u = 0;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+// Composite sort key, ascending = best first: value descending, id ascending.
+__device__ __forceinline__ uint64_t composite(uint32_t key, uint32_t low) {
+    return (static_cast<uint64_t>(~key) << 32) | low;
+}
+
+// ---- glibc expf, bit for bit ---------------------------------------------------
+// Rust's f32::exp calls glibc expf on linux-gnu (sampler.rs:234).  glibc's
+// expf (sysdeps/ieee754/flt-32/e_expf.c, Szabolcs Nagy's method) evaluates
+// 2^(k/32) * 2^(r/32) in double with a 32-entry table and a cubic, and its
+// x86-64 FMA build fuses r = x*N/ln2 - k and the polynomial.  This is the same
+// method, written out with the same fused operations; it was checked against
+// the host's glibc expf on every float in [-104, 88.8] (2.24e9 inputs, 0
+// mismatches) and tests/test_gpu_parity.py re-checks it on the device.
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
+
+__device__ __forceinline__ float glibc_expf(float x) {
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                          // |x| >= 88 or x is nan/inf
+        if (ux == 0xff800000u) return 0.0f;           // exp(-inf) = 0
+        if (abstop >= 0x7f8u) return x + x;           // +inf or nan
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);  // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;          // underflow to +0
+    }
+    const double invln2n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = static_cast<double>(x);
+    const double z = invln2n * xd;
+    double kd = z + shift;
+    const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
+    kd -= shift;
+    const double r = __builtin_fma(invln2n, xd, -kd);
+    uint64_t t = kExp2Tab[ki % 32];
+    t += ki << 47;
+    const double s = __longlong_as_double(static_cast<long long>(t));
+    const double zz = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(zz, r2, y);
+    y = y * s;
+    return static_cast<float>(y);
+}
+
+// ---- wave / block primitives (wave64) -----------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t w = __shfl_xor(v, o, kWave);
+        v = w < v ? w : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        uint32_t w = __shfl_up(v, o, kWave);
+        if (lane >= o) v += w;
+    }
+    return v;
+}
+
+// Exclusive prefix sum over the block; `tmp` holds >= nwaves+1 words of LDS.
+// Returns the prefix; *total gets the block sum.  Contains two barriers.
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* tmp, uint32_t* total) {
+    constexpr int NW = NT / kWave;
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    uint32_t inc = wave_incl_scan(v);
+    if (lane == kWave - 1) tmp[wid] = inc;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        uint32_t t = tmp[w];
+        before += (w < wid) ? t : 0u;
+        all += t;
+    }
+    __syncthreads();
+    *total = all;
+    return before + inc - v;
+}
+
+template <int NT>
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* tmp) {
+    constexpr int NW = NT / kWave;
+    v = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) tmp[threadIdx.x / kWave] = v;
+    __syncthreads();
+    uint32_t all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) all += tmp[w];
+    __syncthreads();
+    return all;
+}
+
+template <int NT>
+__device__ __forceinline__ uint32_t block_min(uint32_t v, uint32_t* tmp) {
+    constexpr int NW = NT / kWave;
+    v = wave_min(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) tmp[threadIdx.x / kWave] = v;
+    __syncthreads();
+    uint32_t all = 0xFFFFFFFFu;
+#pragma unroll
+    for (int w = 0; w < NW; w++) all = tmp[w] < all ? tmp[w] : all;
+    __syncthreads();
+    return all;
+}
+
+// Finds, in a histogram of kBins counts laid out by ascending digit, the
+// first digit whose inclusive cumulative count reaches `need` (>= 1).
+// Writes {digit, count strictly before it} to out[0..1]; leaves out untouched
+// when the total is below `need`.  Block of NT threads, NT * per == kBins.
+template <int NT>
+__device__ __forceinline__ void hist_find(const uint32_t* hist, uint32_t need, uint32_t* tmp,
+                                          uint32_t* out) {
+    constexpr int per = kBins / NT;
+    const int t = threadIdx.x;
+    uint32_t c[per];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < per; i++) {
+        c[i] = hist[t * per + i];
+        sum += c[i];
+    }
+    uint32_t total;
+    uint32_t before = block_excl_scan<NT>(sum, tmp, &total);
+    if (before < need && before + sum >= need) {
+        uint32_t run = before;
+#pragma unroll
+        for (int i = 0; i < per; i++) {
+            if (run + c[i] >= need) {
+                out[0] = t * per + i;
+                out[1] = run;
+                break;
+            }
+            run += c[i];
+        }
+    }
+    __syncthreads();
+}
+
+}  // namespace tsm

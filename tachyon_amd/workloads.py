@@ -62,20 +62,21 @@ class Workload:
         return 0 if self.mask is None else int(self.mask.shape[1])
 
     def algorithmic_bytes(self) -> int:
-        """Bytes one step must move at least: one read of every usable logit,
-        the mask words of constrained rows, the history ids and offsets, the
-        parameters and uniforms, and the outputs written."""
+        """Bytes one step must move at least (BASELINE.md's count): one read
+        of every usable logit, the mask words of constrained rows, the history
+        ids, the uniforms, and the outputs (token, plus logprob and n top
+        (id, logprob) pairs for rows that ask for logprobs)."""
         rows = self.rows
         b = rows * self.usable * 4
         if self.mask is not None:
             nc = int(np.count_nonzero(self.params["flags"] & ROW_CONSTRAINED))
             b += nc * ((self.usable + 31) // 32) * 4
         if self.hist_ids is not None:
-            b += self.hist_ids.size * 4 + (rows + 1) * 4
-        b += rows * (ROW_PARAMS_DTYPE.itemsize + 4)          # params + uniform
+            b += self.hist_ids.size * 4
+        b += rows * 4 + rows * 4  # uniforms in, tokens out
         nlp = self.params["n_logprobs"].astype(np.int64)
         lp_rows = (self.params["flags"] & ROW_LOGPROBS) != 0
-        b += rows * 4 + int(np.sum(np.where(lp_rows, 4 + 8 * nlp, 0)))  # token, logprob, top
+        b += int(np.sum(np.where(lp_rows, 4 + 8 * nlp, 0)))
         return int(b)
 
 

@@ -1,0 +1,89 @@
+"""The C ABI without a GPU: the library builds, loads and exports every
+function include/tachyon_sampler.h declares; the struct layouts seen by a C
+compiler match the ctypes mirror; argument errors come back as messages."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from tachyon_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tachyon_sampler.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:[\w\*]+\s+)+\**(tsm_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert set(names) == set(_lib.SYMBOLS), names
+    for name in names:
+        assert hasattr(L, name), name
+    assert L.tsm_version().decode().startswith("tachyon-sampler")
+
+
+def test_static_archive_has_the_symbols():
+    a = os.path.join(ROOT, "tachyon_amd", "lib", "libtachyon_sampler.a")
+    out = subprocess.run(["nm", "-g", "--defined-only", a], capture_output=True, text=True, check=True).stdout
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}\b", out), name
+
+
+def test_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(f'''
+#include <stdio.h>
+#include <stddef.h>
+#include "{HEADER}"
+int main(void) {{
+  printf("%zu %zu %zu\\n", sizeof(tsm_row_params), sizeof(tsm_batch), sizeof(tsm_outputs));
+  printf("%zu %zu %zu %zu\\n", offsetof(tsm_batch, params), offsetof(tsm_batch, uniforms),
+         offsetof(tsm_outputs, top_stride), offsetof(tsm_outputs, keep));
+  return 0;
+}}''')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
+    l1, l2 = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")[:2]
+    from tachyon_amd.workloads import ROW_PARAMS_DTYPE
+
+    assert [int(v) for v in l1.split()] == [ROW_PARAMS_DTYPE.itemsize, ctypes.sizeof(_lib.TsmBatch),
+                                            ctypes.sizeof(_lib.TsmOutputs)]
+    assert [int(v) for v in l2.split()] == [_lib.TsmBatch.params.offset, _lib.TsmBatch.uniforms.offset,
+                                            _lib.TsmOutputs.top_stride.offset, _lib.TsmOutputs.keep.offset]
+
+
+def _no_gpu():
+    try:
+        import torch
+
+        return not torch.cuda.is_available()
+    except Exception:
+        return True
+
+
+@pytest.mark.skipif(not _no_gpu(), reason="checks the no-device error path")
+def test_create_without_a_device_reports_an_error():
+    L = _lib.lib()
+    err = ctypes.create_string_buffer(256)
+    h = L.tsm_create(0, 16, 1000, err, len(err))
+    assert not h
+    assert err.value  # a message, not a crash
+
+
+def test_argument_errors_need_no_device():
+    L = _lib.lib()
+    err = ctypes.create_string_buffer(256)
+    assert not L.tsm_create(0, 0, 1000, err, len(err))
+    assert b"max_rows" in err.value
+    assert not L.tsm_create(0, 16, 0, err, len(err))
+    assert b"max_vocab" in err.value
+    assert L.tsm_sample(None, None, None, None, err, len(err)) != 0
+    assert L.tsm_distribution(None, None, None, None, None, 0, None, err, len(err)) != 0
+    assert L.tsm_status(None, None, err, len(err)) != 0
+    L.tsm_destroy(None)
