@@ -147,11 +147,14 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
  * Waits for the context's last call and returns its device-side status:
  * 0 when every row was sampled by the specified rule, otherwise TSM_STATUS_*
  * bits (e.g. a history row longer than TSM_MAX_HISTORY, whose counts are
- * then capped).  Clears the status.
+ * then capped, or a row whose n_logprobs exceeds top_stride, whose list is
+ * then cut to top_stride).  Clears the status.
  */
 #define TSM_STATUS_HISTORY_TOO_LONG 1u
 #define TSM_STATUS_BAD_PARAMS       2u
 #define TSM_STATUS_DIST_TRUNCATED   4u
+#define TSM_STATUS_INTERNAL         8u /* a selection found no element (e.g. a
+                                          row of NaN logits); token 0 written */
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);
 
 /* Library version string, e.g. "tachyon-sampler 0.1 gfx950". */

@@ -28,8 +28,10 @@ constexpr uint32_t kOffC = kOffB + kExactCap * 12;     //  8 KB: P, q  | gather 
 constexpr uint32_t kOffD = kOffC + kExactCap * 8;      // 24 KB: histogram counts + f64 mass
 constexpr uint32_t kOffE = kOffD + kBins * 12;         // chunk prefix offsets
 constexpr uint32_t kMaxChunks = TSM_MAX_VOCAB / kChunk;
-constexpr uint32_t kOffF = kOffE + (kMaxChunks + 1) * 4;  // raw top-n composites
-constexpr uint32_t kOffG = kOffF + 32 * 8;                // misc words
+constexpr uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
+constexpr uint32_t kOffF = align16(kOffE + (kMaxChunks + 1) * 4);  // raw top-n composites
+constexpr uint32_t kOffG = kOffF + 32 * 8;                         // misc words (f64 from M_D0)
+static_assert(kOffF % 8 == 0 && (kOffG + 32 * 4) % 8 == 0, "u64/f64 LDS records are 8-byte aligned");
 constexpr uint32_t kMisc = 96;  // 32 scalar words + 32 doubles
 constexpr uint32_t kSmem = kOffG + kMisc * 4 + 32 * 4;    // + scan tmp
 static_assert(kSmem <= 160 * 1024, "LDS budget");
@@ -215,6 +217,34 @@ __device__ __forceinline__ uint64_t select_kth(Fin& f, const Filt& q, uint32_t k
     return select_from(f, q, k, 0, 0, 64);
 }
 
+// The filtered element with the largest composite <= T, or ~0 when there is
+// none.  select_kth / mass_select return a threshold whose low bits may be
+// padding; this resolves it to the element itself (its id is the low word).
+__device__ uint64_t exact_at(Fin& f, const Filt& q, uint64_t T) {
+    unsigned long long best = 0;
+    uint32_t any = 0;
+    row_pass(f, [&](uint32_t id, float x, float y) {
+        const uint64_t c = comp_of(q.order, id, x, y);
+        if (c <= T && keep_el(f, q, id, y, c) && (!any || c > best)) {
+            best = c;
+            any = 1;
+        }
+    });
+    best = any ? best + 1ull : 0ull;  // 0 = nothing; composites fit below ~0
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long w = __shfl_xor(best, o, kWave);
+        best = w > best ? w : best;
+    }
+    unsigned long long* wtmp = reinterpret_cast<unsigned long long*>(f.miscd + 8);
+    if ((threadIdx.x & (kWave - 1)) == 0) wtmp[threadIdx.x / kWave] = best;
+    __syncthreads();
+    unsigned long long all = 0;
+    for (int w = 0; w < kFinThreads / kWave; w++) all = wtmp[w] > all ? wtmp[w] : all;
+    __syncthreads();
+    return all == 0 ? ~0ull : all - 1ull;
+}
+
 // Block-wide exclusive f64 scan (1024 threads).
 __device__ double block_excl_scan_f64(double v, double* tmp, double* total) {
     constexpr int NW = kFinThreads / kWave;
@@ -290,7 +320,8 @@ __device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
         if (c0 + c1 > 0) atomicMax(&f.misc[M_FIND2], (c1 > 0 ? b0 + 1 : b0) + 1);  // last nonempty + 1
         __syncthreads();
         uint32_t d = f.misc[M_FIND];
-        if (d == 0xFFFFFFFFu) d = f.misc[M_FIND2] - 1;  // target beyond the total: last element
+        const bool overshoot = d == 0xFFFFFFFFu;  // read now: select_from below rewrites M_FIND
+        if (overshoot) d = f.misc[M_FIND2] - 1;   // target beyond the total: last element
         if ((d >> 1) == tid) {
             const bool second = d & 1u;
             f.miscd[0] = base + (second ? m0 : 0.0);
@@ -311,7 +342,7 @@ __device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
             const double pk = static_cast<double>(glibc_expf((yk - y0) / f.m.t));
             double need_d = pk > 0.0 ? ceil((target - cum_before) / pk) : 1.0;
             uint32_t need = need_d < 1.0 ? 1u : (need_d > static_cast<double>(ties) ? ties : static_cast<uint32_t>(need_d));
-            if (f.misc[M_FIND] == 0xFFFFFFFFu) need = ties;  // overshoot: take the last
+            if (overshoot) need = ties;  // take the last
             MassSel s;
             s.T = (need == ties) ? (known | 0xFFFFFFFFull) : select_from(f, q, need, 3, known, 32);
             s.cum = cum_before + static_cast<double>(need) * pk;
@@ -496,7 +527,7 @@ __device__ uint32_t slow_fallback(Fin& f, uint32_t n_allowed) {
 }
 
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(FinArgs a) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
+    HIP_DYNAMIC_SHARED(unsigned char, smem_raw)
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const uint32_t n = a.usable;
     const tsm_row_params P = a.params[row];
@@ -615,6 +646,10 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(FinArgs a) {
     bool raw_ok = false;
     uint32_t nraw = 0;
     const bool want_lp = m.logprobs && a.out_top_ids != nullptr && m.nlp > 0;
+    if (want_lp && m.nlp > a.top_stride) {  // the list must fit the row's slots
+        if (tid == 0) atomicOr(a.status, TSM_STATUS_BAD_PARAMS);
+        f.m.nlp = a.top_stride;
+    }
     if (want_lp && cand_ok && !(fl_or & CS_PEN_OVERFLOW) && npen_tot + m.nlp <= kMergeCap) {
         // (a) first nlp non-penalized entries of the sorted list
         if (tid == 0) {
@@ -672,7 +707,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(FinArgs a) {
         } else {
             Filt q;
             q.order = ORD_CANON_X;
-            tok = static_cast<uint32_t>(select_kth(f, q, 1));
+            tok = static_cast<uint32_t>(exact_at(f, q, select_kth(f, q, 1)));
         }
         pk.token = tok;
         pk.keep = 0;
@@ -856,8 +891,9 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(FinArgs a) {
                     return;
                 }
                 const MassSel sr = mass_select(f, q3, y0, static_cast<double>(u) * mass);
-                const uint32_t ktok = static_cast<uint32_t>(sr.T);
-                const float yk = key_to_float(~static_cast<uint32_t>(sr.T >> 32));
+                const uint64_t ce = exact_at(f, q3, sr.T);
+                const uint32_t ktok = static_cast<uint32_t>(ce);
+                const float yk = key_to_float(~static_cast<uint32_t>(ce >> 32));
                 pk.token = ktok;
                 pk.keep = keep;
                 pk.prob = static_cast<float>(static_cast<double>(glibc_expf((yk - y0) / m.t)) / mass);
@@ -867,6 +903,10 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(FinArgs a) {
     }
 
     // ---- 5. outputs ----
+    if (pk.token >= n) {  // a selection came back empty (e.g. NaN logits)
+        if (tid == 0) atomicOr(a.status, TSM_STATUS_INTERNAL);
+        pk.token = 0;
+    }
     if (a.distribution) {
         if (pk.keep > 0) write_dist_exact(f, a, row, pk);
         if (tid == 0) a.out_keep[row] = pk.keep;

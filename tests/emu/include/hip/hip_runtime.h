@@ -1,0 +1,213 @@
+// hip_runtime.h - CPU emulation of the subset of HIP the sampling kernels use.
+// TEST INFRASTRUCTURE ONLY: tests/emu builds the product kernel sources
+// (tachyon_amd/csrc/*.hip) against this header with g++ and AddressSanitizer /
+// UndefinedBehaviorSanitizer (or ThreadSanitizer), so that an out-of-bounds
+// access, a misaligned vector load or a missing barrier shows up on the CPU
+// instead of faulting a GPU.  Nothing in the product links this.
+//
+// Model: a launch runs its blocks one after another; the threads of a block
+// are OS threads.  __syncthreads() is a block-wide barrier that also checks
+// every live thread reached the same source line; a thread that returns from
+// the kernel stops counting for the rest of its block (as an ended wave does
+// on the GPU).  Shuffles exchange through a per-wave (64-lane) barrier.
+// __shared__ variables are static (blocks never overlap); dynamic shared
+// memory is a heap buffer of exactly the launch's size, refilled with 0xCD
+// before each block, so an overrun is a heap overflow and a read of LDS that
+// was never written sees garbage.
+#pragma once
+
+#include <atomic>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <tuple>
+#include <utility>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__ static
+#define __constant__ static
+#define __align__(n) alignas(n)
+#define HIP_DYNAMIC_SHARED(type, var) type* var = reinterpret_cast<type*>(::emu::dyn_smem());
+#define __builtin_amdgcn_exp2f(x) exp2f(x)
+#define HIP_SYMBOL(x) (&(x))
+
+struct dim3 {
+    uint32_t x, y, z;
+    constexpr dim3(uint32_t x_ = 1, uint32_t y_ = 1, uint32_t z_ = 1) : x(x_), y(y_), z(z_) {}
+};
+
+struct alignas(16) float4 { float x, y, z, w; };
+struct alignas(8) float2 { float x, y; };
+struct alignas(8) uint2 { uint32_t x, y; };
+struct alignas(16) uint4 { uint32_t x, y, z, w; };
+inline uint2 make_uint2(uint32_t x, uint32_t y) { return uint2{x, y}; }
+inline uint4 make_uint4(uint32_t x, uint32_t y, uint32_t z, uint32_t w) { return uint4{x, y, z, w}; }
+inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
+
+namespace emu {
+#ifdef EMU_THREADS
+#define EMU_TLS thread_local
+#else
+#define EMU_TLS  // fibers share one OS thread; the scheduler sets these per switch
+#endif
+extern EMU_TLS dim3 t_threadIdx, t_blockIdx;
+extern dim3 g_blockDim, g_gridDim;
+unsigned char* dyn_smem();
+void syncthreads(const char* file, int line);
+void wave_sync();
+uint64_t* wave_slots();
+int next_bank();  // this lane's shuffle count parity, then advances it
+int lane_id();
+using Body = std::function<void()>;
+void run_launch(dim3 grid, dim3 block, size_t smem, const Body& body);
+}  // namespace emu
+
+#define threadIdx (::emu::t_threadIdx)
+#define blockIdx (::emu::t_blockIdx)
+#define blockDim (::emu::g_blockDim)
+#define gridDim (::emu::g_gridDim)
+#define __syncthreads() ::emu::syncthreads(__FILE__, __LINE__)
+
+#include <type_traits>
+template <class T, class U>
+inline std::common_type_t<T, U> min(T a, U b) { return a < b ? a : b; }
+template <class T, class U>
+inline std::common_type_t<T, U> max(T a, U b) { return a > b ? a : b; }
+
+inline uint32_t __float_as_uint(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
+inline float __uint_as_float(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
+inline int __float_as_int(float f) { int u; std::memcpy(&u, &f, 4); return u; }
+inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; }
+inline long long __double_as_longlong(double d) { long long u; std::memcpy(&u, &d, 8); return u; }
+inline double __longlong_as_double(long long u) { double d; std::memcpy(&d, &u, 8); return d; }
+inline int __popc(uint32_t v) { return __builtin_popcount(v); }
+inline int __popcll(uint64_t v) { return __builtin_popcountll(v); }
+inline int __clz(uint32_t v) { return v ? __builtin_clz(v) : 32; }
+inline int __ffs(uint32_t v) { return __builtin_ffs(v); }
+
+template <class T>
+inline T emu_shfl(T v, int src) {
+    static_assert(sizeof(T) <= 8, "shuffle of <= 8 bytes");
+    // Two slot banks used alternately: a lane writes bank b only after the
+    // wave's previous shuffle (bank b^1) released, and every lane finished
+    // reading bank b two shuffles ago, so one wave barrier per shuffle is enough.
+    uint64_t* slots = ::emu::wave_slots();
+    const int lane = ::emu::lane_id();
+    uint64_t bits = 0;
+    std::memcpy(&bits, &v, sizeof(T));
+    const int bank = ::emu::next_bank();
+    slots[bank * 64 + lane] = bits;
+    ::emu::wave_sync();
+    T r;
+    const uint64_t got = slots[bank * 64 + src];
+    std::memcpy(&r, &got, sizeof(T));
+    return r;
+}
+template <class T>
+inline T __shfl_xor(T v, int mask, int width = 64) {
+    const int lane = ::emu::lane_id();
+    int src = lane ^ mask;
+    if ((src & ~(width - 1)) != (lane & ~(width - 1))) src = lane;
+    return emu_shfl(v, src);
+}
+template <class T>
+inline T __shfl_up(T v, unsigned delta, int width = 64) {
+    const int lane = ::emu::lane_id();
+    const int seg = lane & ~(width - 1);
+    int src = lane - static_cast<int>(delta);
+    if (src < seg) src = lane;
+    return emu_shfl(v, src);
+}
+template <class T>
+inline T __shfl_down(T v, unsigned delta, int width = 64) {
+    const int lane = ::emu::lane_id();
+    const int seg = lane & ~(width - 1);
+    int src = lane + static_cast<int>(delta);
+    if (src >= seg + width) src = lane;
+    return emu_shfl(v, src);
+}
+template <class T>
+inline T __shfl(T v, int src, int width = 64) {
+    const int lane = ::emu::lane_id();
+    return emu_shfl(v, (lane & ~(width - 1)) + (src & (width - 1)));
+}
+
+template <class T>
+inline T atomicAdd(T* p, T v) { return std::atomic_ref<T>(*p).fetch_add(v); }
+template <class T>
+inline T atomicOr(T* p, T v) { return std::atomic_ref<T>(*p).fetch_or(v); }
+template <class T>
+inline T atomicAnd(T* p, T v) { return std::atomic_ref<T>(*p).fetch_and(v); }
+template <class T>
+inline T atomicExch(T* p, T v) { return std::atomic_ref<T>(*p).exchange(v); }
+template <class T>
+inline T atomicMin(T* p, T v) {
+    std::atomic_ref<T> a(*p);
+    T old = a.load();
+    while (v < old && !a.compare_exchange_weak(old, v)) {}
+    return old;
+}
+template <class T>
+inline T atomicMax(T* p, T v) {
+    std::atomic_ref<T> a(*p);
+    T old = a.load();
+    while (v > old && !a.compare_exchange_weak(old, v)) {}
+    return old;
+}
+template <class T>
+inline T atomicCAS(T* p, T cmp, T v) {
+    std::atomic_ref<T>(*p).compare_exchange_strong(cmp, v);
+    return cmp;
+}
+
+// ---- runtime ----
+typedef enum hipError_t {
+    hipSuccess = 0,
+    hipErrorInvalidValue = 1,
+    hipErrorOutOfMemory = 2,
+    hipErrorInvalidDevice = 101,
+    hipErrorLaunchFailure = 719,
+} hipError_t;
+typedef struct ihipStream_t* hipStream_t;
+enum hipMemcpyKind { hipMemcpyHostToHost, hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice,
+                     hipMemcpyDefault };
+enum hipFuncAttribute { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
+struct hipDeviceProp_t {
+    char name[256];
+    char gcnArchName[256];
+    int multiProcessorCount;
+    size_t sharedMemPerBlock;
+};
+
+hipError_t hipMalloc(void** p, size_t n);
+template <class T>
+inline hipError_t hipMalloc(T** p, size_t n) { return hipMalloc(reinterpret_cast<void**>(p), n); }
+hipError_t hipFree(void* p);
+hipError_t hipMemset(void* p, int v, size_t n);
+hipError_t hipMemsetAsync(void* p, int v, size_t n, hipStream_t s = nullptr);
+hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind k);
+hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind k, hipStream_t st = nullptr);
+hipError_t hipGetDeviceCount(int* n);
+hipError_t hipSetDevice(int d);
+hipError_t hipGetDevice(int* d);
+hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d);
+hipError_t hipDeviceSynchronize();
+hipError_t hipStreamSynchronize(hipStream_t s);
+hipError_t hipGetLastError();
+const char* hipGetErrorString(hipError_t e);
+hipError_t hipFuncSetAttribute(const void* f, hipFuncAttribute a, int v);
+hipError_t hipGetSymbolAddress(void** p, const void* sym);
+
+template <class... KA, class... A>
+inline void hipLaunchKernelGGL(void (*k)(KA...), dim3 grid, dim3 block, size_t smem, hipStream_t, A&&... args) {
+    std::tuple<KA...> t(std::forward<A>(args)...);
+    ::emu::run_launch(grid, block, smem, [k, t]() { std::apply(k, t); });
+}

@@ -1,0 +1,78 @@
+"""The HIP kernels' logic on the CPU: the product kernel sources compiled
+against the HIP emulation of tests/emu (AddressSanitizer + UBSan, every
+"device" array its own exact-size allocation, barriers checked for
+divergence), run through the C ABI and held to the same parity bars as the
+GPU tests.  This is how a kernel change is checked before it runs on a GPU.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import emu_harness as E
+from parity import DIST_CASES, RANDOM_CASES, check, check_distribution, check_mask_property
+from tachyon_amd import workloads as wl
+
+# the small cases run here; the wide ones (vocab >= 20000) run with TSM_EMU_ALL=1
+FAST = [c for c in RANDOM_CASES if c["vocab"] < 20000]
+WIDE = [c for c in RANDOM_CASES if c["vocab"] >= 20000]
+ALL = os.environ.get("TSM_EMU_ALL") == "1"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def driver():
+    return E.build()
+
+
+def run_case(w, label):
+    from oracle import pyoracle
+
+    got = E.emu_sample(w)
+    assert got["status"] == 0, got["status"]
+    ref = pyoracle.sample_batch(w)
+    check(w, got, ref, label)
+    check_mask_property(w, got)
+    return got, ref
+
+
+@pytest.mark.parametrize("case", FAST, ids=[f"rand{c['seed']}" for c in FAST])
+def test_emu_parity_random(case):
+    run_case(wl.random_case(**case), f"emu rand{case['seed']}")
+
+
+@pytest.mark.skipif(not ALL, reason="wide cases take minutes on the emulation; TSM_EMU_ALL=1 runs them")
+@pytest.mark.parametrize("case", WIDE, ids=[f"rand{c['seed']}" for c in WIDE])
+def test_emu_parity_random_wide(case):
+    run_case(wl.random_case(**case), f"emu rand{case['seed']}")
+
+
+@pytest.mark.parametrize("name,rows", [("c1", 1), ("c2", 8), ("c3", 4), ("c4", 4), ("c5", 4)])
+def test_emu_parity_configs(name, rows):
+    """BASELINE shapes at full vocabulary with few rows.  c2's rows come in
+    blocks of 8 per kind, so it takes every 4th row of the full batch to
+    keep two rows of each kind."""
+    if name == "c2":
+        full = wl.c2()
+        sel = np.arange(0, 32, 4)
+        w = wl.Workload("c2s", full.logits[sel], full.usable, full.params[sel], None, None, None,
+                        full.uniforms[sel])
+        lens = np.diff(full.hist_offsets)[sel]
+        off = np.zeros(len(sel) + 1, np.uint32)
+        off[1:] = np.cumsum(lens)
+        w.hist_ids = np.concatenate([full.hist_ids[full.hist_offsets[r]:full.hist_offsets[r + 1]] for r in sel])
+        w.hist_offsets = off
+    elif name == "c1":
+        w = wl.c1()
+    else:
+        w = wl.CONFIGS[name](rows=rows)
+    run_case(w, f"emu {name}")
+
+
+def test_emu_distribution():
+    from oracle import pyoracle
+
+    for seed, kw in DIST_CASES:
+        w = wl.random_case(seed=seed, rows=12, **kw)
+        got = E.emu_distribution(w, 1024)
+        rids, rps, rkeep = pyoracle.distribution_batch(w, 1024)
+        check_distribution(w, got["ids"], got["probs"], got["keep"], rids, rps, rkeep, f"emu dist{seed}")

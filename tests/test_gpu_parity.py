@@ -23,9 +23,7 @@ from tachyon_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
 
-TOL_U = 1e-5
-TOL_P = 1e-5
-EXACT_CAP = 1024
+from parity import DIST_CASES, RANDOM_CASES, check, check_distribution, check_mask_property
 
 
 def say(msg):
@@ -43,48 +41,6 @@ def ctx():
     c = SamplerContext(max_rows=1024, max_vocab=152064)
     yield c
     c.close()
-
-
-def close(a, b, rel=1e-5, abs_=1e-6):
-    return abs(float(a) - float(b)) <= abs_ + rel * abs(float(b))
-
-
-def check(w, got, ref, label):
-    """Returns (n_exact_rows, n_boundary_exempt)."""
-    from oracle import pyoracle
-
-    exempt = 0
-    exact_rows = 0
-    for r in range(w.rows):
-        d = ref.diag[r]
-        p = w.params[r]
-        tag = f"{label} row {r} params={p} diag={d}"
-        exact = d["path"] in (pyoracle.PATH_ARGMAX_FAST, pyoracle.PATH_NONE_ALLOWED) or d["survivors"] <= EXACT_CAP
-        if exact:
-            exact_rows += 1
-            assert got["token"][r] == ref.token[r], tag + f" gpu={got['token'][r]} ref={ref.token[r]}"
-            assert got["keep"][r] == ref.keep[r], tag + f" gpu keep={got['keep'][r]}"
-            assert got["prob"][r].tobytes() == ref.prob[r].tobytes(), tag + f" prob {got['prob'][r]} {ref.prob[r]}"
-            same_token = True
-        else:
-            boundary = d["u_gap"] < TOL_U or d["p_gap"] < TOL_P
-            same_token = got["token"][r] == ref.token[r]
-            if not same_token:
-                assert boundary, tag + f" gpu={got['token'][r]} ref={ref.token[r]}"
-                exempt += 1
-            if got["keep"][r] != ref.keep[r]:
-                assert d["p_gap"] < TOL_P or got["keep"][r] == d["keep_exact"], tag + f" keep {got['keep'][r]}"
-            if same_token and got["keep"][r] == ref.keep[r]:
-                # against the exact-arithmetic probability p_pick / sum(p)
-                p_exact = float(ref.prob[r]) * float(d["mass"]) / float(d["mass64"])
-                assert close(got["prob"][r], p_exact), tag + f" prob {got['prob'][r]} vs {p_exact}"
-        if (p["flags"] & wl.ROW_LOGPROBS) and same_token:
-            assert close(got["logprob"][r], ref.logprob[r]), tag + f" lp {got['logprob'][r]} {ref.logprob[r]}"
-            n = min(int(p["n_logprobs"]), w.usable, w.top_stride)
-            assert got["top_ids"][r, :n].tolist() == ref.top_ids[r, :n].tolist(), tag
-            for j in range(n):
-                assert close(got["top_lp"][r, j], ref.top_lp[r, j]), tag + f" top lp {j}"
-    return exact_rows, exempt
 
 
 def run_case(ctx, w, label, nthreads=16):
@@ -116,7 +72,7 @@ def test_device_expf_matches_glibc(ctx):
     neg = np.arange(0x80000000, 0xC2D00000, 97, dtype=np.uint64).astype(np.uint32).view(np.float32)
     pos = np.arange(0, 0x42B20000, 97, dtype=np.uint64).astype(np.uint32).view(np.float32)
     special = np.array([0.0, -0.0, np.inf, -np.inf, 88.0, -88.0, 88.72283, 88.72284, -103.97208, -103.97207,
-                        0x1.04845ep+5, -0x1.f8cbb2p+5, 1e-30, -1e-30, -87.33655, -87.3366], np.float32)
+                        float.fromhex('0x1.04845ep+5'), float.fromhex('-0x1.f8cbb2p+5'), 1e-30, -1e-30, -87.33655, -87.3366], np.float32)
     x = np.concatenate([neg, pos, special]).astype(np.float32)
     say(f"[gpu] expf sweep over {x.size} inputs")
     xd = torch.from_numpy(x).cuda()
@@ -130,25 +86,6 @@ def test_device_expf_matches_glibc(ctx):
     assert bad.size == 0, [(float(x[i]), float(got[i]), float(ref[i])) for i in bad[:5]]
 
 
-RANDOM_CASES = [
-    dict(seed=1, vocab=300),
-    dict(seed=2, vocab=300, ties=True),
-    dict(seed=3, vocab=300, masked=True),
-    dict(seed=4, vocab=300, masked=True, ties=True, mask_frac=0.05),
-    dict(seed=5, vocab=1500, masked=True, mask_frac=0.02, rows=12),
-    dict(seed=6, vocab=2100, rows=12, mode="nucleus"),
-    dict(seed=7, vocab=2100, rows=12, mode="minp", ties=True),
-    dict(seed=8, vocab=64, rows=12, stride=80, masked=True, ties=True),
-    dict(seed=9, vocab=1200, rows=12, mode="topp", sigma=8.0),
-    dict(seed=10, vocab=5, rows=12, masked=True, mask_frac=0.6),
-    dict(seed=11, vocab=40000, rows=24, masked=True, mask_frac=0.01),
-    dict(seed=12, vocab=40000, rows=24, ties=True, hist_len=300),
-    dict(seed=13, vocab=20001, rows=18, stride=20003, masked=True),
-    dict(seed=14, vocab=70000, rows=12, mode="nucleus", sigma=1.0),
-    dict(seed=15, vocab=70000, rows=12, mode="all", masked=True, mask_frac=0.002),
-]
-
-
 @pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"rand{c['seed']}" for c in RANDOM_CASES])
 def test_parity_random(ctx, case):
     w = wl.random_case(**case)
@@ -159,11 +96,7 @@ def test_parity_random(ctx, case):
 def test_parity_baseline_configs(ctx, name):
     w = wl.CONFIGS[name]()
     got, ref = run_case(ctx, w, name)
-    if w.mask is not None:  # size-independent property: every pick is allowed
-        for r in range(w.rows):
-            t = int(got["token"][r])
-            if got["keep"][r] > 0:
-                assert (w.mask[r, t >> 5] >> (t & 31)) & 1
+    check_mask_property(w, got)
 
 
 def test_parity_c5_nucleus(ctx):
@@ -185,25 +118,20 @@ def test_repeat_calls_are_identical(ctx):
 
 
 def test_distribution_parity(ctx):
+    import torch
+
     from oracle import pyoracle
     from tachyon_amd.device import upload
 
-    for seed, kw in [(21, dict(vocab=500, mode="mixed")), (22, dict(vocab=3000, mode="minp")),
-                     (23, dict(vocab=3000, mode="topk", ties=True))]:
+    for seed, kw in DIST_CASES:
         w = wl.random_case(seed=seed, rows=12, **kw)
         say(f"[gpu] distribution seed {seed}")
         b = upload(w)
         ids, ps, keep = ctx.distribution(b, 1024)
-        import torch
-
         torch.cuda.synchronize()
         ids, ps, keep = ids.cpu().numpy().view(np.uint32), ps.cpu().numpy(), keep.cpu().numpy().view(np.uint32)
         rids, rps, rkeep = pyoracle.distribution_batch(w, 1024)
-        for r in range(w.rows):
-            assert keep[r] == rkeep[r], (seed, r)
-            k = min(int(keep[r]), 1024)
-            assert ids[r, :k].tolist() == rids[r, :k].tolist(), (seed, r)
-            assert np.array_equal(ps[r, :k], rps[r, :k]), (seed, r)
+        check_distribution(w, ids, ps, keep, rids, rps, rkeep, f"dist{seed}")
 
 
 def test_abi_rejects_bad_arguments(ctx):
