@@ -148,7 +148,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_step": alg_bytes,
-                     "kernel": "one tsm_sample step: sweep_kernel + finalize_kernel"},
+                     "kernel": "sample_kernel (one launch per tsm_sample step)"},
         "cpu_baseline": cpu,
     }
     ctx.close()

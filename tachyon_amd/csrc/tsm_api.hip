@@ -1,19 +1,15 @@
 // tsm_api.hip - the C ABI (include/tachyon_sampler.h): context, argument
-// checks on the host, and the two launches of a step on the caller's stream.
+// checks on the host, and the one launch of a step on the caller's stream.
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 
-#include "tsm_launch.h"
+#include "tsm_sample.h"
 
 struct tsm_ctx {
     int device;
-    uint32_t max_rows, max_vocab, max_chunks;
-    tsm::ChunkStats* stats;
-    uint2* cand;
-    uint2* pen;
-    uint2* allow;
-    uint32_t* status;
+    uint32_t max_rows, max_vocab;
+    uint32_t* status;  // TSM_STATUS_* bits of the calls since the last tsm_status()
 };
 
 namespace {
@@ -99,20 +95,12 @@ tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err
     c->device = device;
     c->max_rows = max_rows;
     c->max_vocab = max_vocab;
-    c->max_chunks = (max_vocab + tsm::kChunk - 1) / tsm::kChunk;
-    const size_t slots = static_cast<size_t>(max_rows) * c->max_chunks;
-    hipError_t e = hipSuccess;
-    e = hipMalloc(&c->stats, slots * sizeof(tsm::ChunkStats));
-    if (e == hipSuccess) e = hipMalloc(&c->cand, slots * tsm::kCandCap * sizeof(uint2));
-    if (e == hipSuccess) e = hipMalloc(&c->pen, slots * tsm::kPenCap * sizeof(uint2));
-    if (e == hipSuccess) e = hipMalloc(&c->allow, slots * tsm::kAllowCap * sizeof(uint2));
-    if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(uint32_t));
+    c->status = nullptr;
+    hipError_t e = hipMalloc(&c->status, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
-    if (e == hipSuccess) {
-        e = tsm::finalize_set_smem_attr();
-    }
+    if (e == hipSuccess) e = tsm::sample_set_smem_attr();
     if (e != hipSuccess) {
-        set_err(err, errlen, "device allocation failed: %s", hipGetErrorString(e));
+        set_err(err, errlen, "device setup failed: %s", hipGetErrorString(e));
         tsm_destroy(c);
         return nullptr;
     }
@@ -123,10 +111,6 @@ void tsm_destroy(tsm_ctx* ctx) {
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     (void)hipDeviceSynchronize();
-    if (ctx->stats) (void)hipFree(ctx->stats);
-    if (ctx->cand) (void)hipFree(ctx->cand);
-    if (ctx->pen) (void)hipFree(ctx->pen);
-    if (ctx->allow) (void)hipFree(ctx->allow);
     if (ctx->status) (void)hipFree(ctx->status);
     delete ctx;
 }
@@ -138,63 +122,38 @@ static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs
     DeviceGuard g(ctx->device);
     if (!g.ok) return set_err(err, errlen, "hipSetDevice(%d) failed", ctx->device), 1;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t n_chunks = (b->usable + tsm::kChunk - 1) / tsm::kChunk;
     const bool vec = (b->row_stride % 4 == 0) && aligned16(b->logits);
 
-    tsm::SweepArgs sa;
-    sa.logits = b->logits;
-    sa.params = b->params;
-    sa.hist_ids = b->hist_ids;
-    sa.hist_off = b->hist_offsets;
-    sa.mask = distribution ? nullptr : b->mask;
-    sa.stats = ctx->stats;
-    sa.cand = ctx->cand;
-    sa.pen = ctx->pen;
-    sa.allow = ctx->allow;
-    sa.status = ctx->status;
-    sa.row_stride = b->row_stride;
-    sa.usable = b->usable;
-    sa.mask_stride = b->mask_stride;
-    sa.n_chunks = n_chunks;
-
-    tsm::FinArgs fa;
-    std::memset(&fa, 0, sizeof(fa));
-    fa.logits = b->logits;
-    fa.params = b->params;
-    fa.hist_ids = b->hist_ids;
-    fa.hist_off = b->hist_offsets;
-    fa.mask = sa.mask;
-    fa.uniforms = b->uniforms;
-    fa.stats = ctx->stats;
-    fa.cand = ctx->cand;
-    fa.pen = ctx->pen;
-    fa.allow = ctx->allow;
-    fa.status = ctx->status;
-    fa.row_stride = b->row_stride;
-    fa.usable = b->usable;
-    fa.mask_stride = b->mask_stride;
-    fa.n_chunks = n_chunks;
-    fa.distribution = distribution ? 1u : 0u;
+    tsm::SampleArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.logits = b->logits;
+    a.params = b->params;
+    a.hist_ids = b->hist_ids;
+    a.hist_off = b->hist_offsets;
+    a.mask = distribution ? nullptr : b->mask;
+    a.uniforms = b->uniforms;
+    a.status = ctx->status;
+    a.row_stride = b->row_stride;
+    a.usable = b->usable;
+    a.mask_stride = b->mask_stride;
+    a.distribution = distribution ? 1u : 0u;
     if (distribution) {
-        fa.dist_ids = dist_ids;
-        fa.dist_probs = dist_probs;
-        fa.dist_stride = dist_stride;
-        fa.out_keep = keep;
+        a.dist_ids = dist_ids;
+        a.dist_probs = dist_probs;
+        a.dist_stride = dist_stride;
+        a.out_keep = keep;
     } else {
-        fa.out_token = out->token;
-        fa.out_logprob = out->logprob;
-        fa.out_top_ids = out->top_ids;
-        fa.out_top_lp = out->top_logprobs;
-        fa.top_stride = out->top_stride;
-        fa.out_prob = out->prob;
-        fa.out_keep = out->keep;
+        a.out_token = out->token;
+        a.out_logprob = out->logprob;
+        a.out_top_ids = out->top_ids;
+        a.out_top_lp = out->top_logprobs;
+        a.top_stride = out->top_stride;
+        a.out_prob = out->prob;
+        a.out_keep = out->keep;
     }
-    tsm::launch_sweep(sa, b->rows, vec, s);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_err(err, errlen, "sweep launch failed: %s", hipGetErrorString(e)), 1;
-    tsm::launch_finalize(fa, b->rows, s);
-    e = hipGetLastError();
-    if (e != hipSuccess) return set_err(err, errlen, "finalize launch failed: %s", hipGetErrorString(e)), 1;
+    tsm::launch_sample(a, b->rows, vec, s);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(err, errlen, "kernel launch failed: %s", hipGetErrorString(e)), 1;
     return 0;
 }
 

@@ -12,40 +12,13 @@ namespace tsm {
 
 // ---- geometry --------------------------------------------------------------
 constexpr int kWave = 64;
-constexpr int kSweepThreads = 256;                        // 4 waves
-constexpr int kSweepVec = 16;                             // float4 per thread
-constexpr uint32_t kChunk = kSweepThreads * kSweepVec * 4;  // 16384 ids per chunk
-constexpr int kGroupVec = 2;                              // float4 per group
-constexpr int kGroups = kSweepVec / kGroupVec;            // 8 groups of 8 per thread
-constexpr uint32_t kCandCap = 2048;    // candidate slots per chunk
-constexpr uint32_t kPenCap = 1024;     // penalized-id slots per chunk
-constexpr uint32_t kAllowCap = 1024;   // allowed-id slots per chunk (sparse masks)
+constexpr int kBlock = 1024;           // one workgroup (16 waves) per row
+constexpr int kVec = 2;                // float4 loads per thread per tile
+constexpr uint32_t kTile = kBlock * kVec * 4;  // 16384 ids per tile
 constexpr uint32_t kMaxWindow = 1024;  // top_n path bound (sampler.rs:193)
 constexpr uint32_t kWideWindow = 256;  // constrained window floor (sampler.rs:186-187)
-constexpr int kFinThreads = 1024;      // 16 waves
-constexpr uint32_t kMergeCap = 4096;   // candidates merged in LDS
-constexpr uint32_t kExactCap = 1024;   // longest list the exact path sorts
-constexpr uint32_t kTile = 16384;      // ids per tile of a re-read pass
+constexpr uint32_t kExactCap = 1024;   // longest ranked list finished exactly
 constexpr uint32_t kBins = 2048;       // radix histogram bins (11-bit digits)
-
-// ---- scratch records -------------------------------------------------------
-enum : uint32_t {
-    CS_HAS_CAND = 1u,       // the chunk wrote candidates
-    CS_CAND_OVERFLOW = 2u,  // more candidates than kCandCap (or Wc > cap)
-    CS_PEN_OVERFLOW = 4u,   // more penalized ids than kPenCap
-    CS_ALLOW_LIST = 8u,     // every allowed id of the chunk is in its list
-};
-
-struct ChunkStats {         // 32 bytes, one per (row, chunk)
-    double raw_sum;         // sum over the chunk of exp(x - raw_max)
-    float raw_max;          // max raw logit of the chunk
-    uint32_t n_cand;        // candidates found (may exceed kCandCap)
-    uint32_t n_pen;         // distinct history ids inside the chunk
-    uint32_t n_allowed;     // mask popcount over the chunk
-    uint32_t flags;         // CS_*
-    uint32_t pad;
-};
-static_assert(sizeof(ChunkStats) == 32, "ChunkStats layout");
 
 // ---- per-row mode (sampler.rs:161-190 + extensions) -------------------------
 struct RowMode {
@@ -158,7 +131,17 @@ __device__ __forceinline__ float glibc_expf(float x) {
     return static_cast<float>(y);
 }
 
+// ---- LDS ----------------------------------------------------------------------
+// Base of the workgroup's dynamic LDS.  Every LDS structure is addressed from
+// here at a fixed offset, so no LDS pointer is ever stored in memory and the
+// compiler always sees LDS accesses (ds_*) rather than generic ones.
+__device__ __forceinline__ unsigned char* lds_base() {
+    HIP_DYNAMIC_SHARED(unsigned char, tsm_lds)
+    return tsm_lds;
+}
+
 // ---- wave / block primitives (wave64) -----------------------------------------
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

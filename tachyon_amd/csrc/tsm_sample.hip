@@ -1,0 +1,808 @@
+// tsm_sample.hip - the sampling kernel: one 1024-thread workgroup per row,
+// one launch per step, no device memory besides the caller's inputs and
+// outputs and one status word.
+//
+// Streaming pass (every row): the workgroup reads its row once, in tiles of
+// float4 loads with the next tile prefetched into registers, and in the same
+// pass
+//   * applies the repetition penalty (sampler.rs:165-175) and the presence /
+//     frequency penalties in registers: the row's history is turned once into
+//     an LDS bitmap of its ids plus a table of their counts;
+//   * reads the tile's packed allow-mask words and counts allowed ids;
+//   * accumulates max and sum exp(x - max) of the raw logits (sampler.rs:
+//     298-304) per thread;
+//   * appends to an LDS candidate buffer every element at or above one of
+//     three running thresholds: the row's window (top-W by penalized value,
+//     sampler.rs:186-194), the best non-penalized values (the raw top-n of
+//     logprobs) and the best allowed values (the whole-vocabulary fallback
+//     of sampler.rs:211-221).  Penalized ids also go to a list with their
+//     raw values.  A threshold starts from a lower bound read off the first
+//     tile's group maxima and is raised to the exact order statistic
+//     whenever the buffer fills, so the buffer ends holding a small superset
+//     of every element the finish can need.
+// Finish: exact radix selects over the buffer give the window, the allowed
+// ids inside it (or the fallback set) and the raw top-n; the ranked list is
+// sorted and finished with the reference's own sequential f32 arithmetic
+// (tsm_select.h: exact_finalize), so tokens are bit-exact.
+//
+// Rows without top-k (window > 1024), rows whose candidates cannot be
+// bounded (pathological ties) and rows whose history does not fit the LDS
+// table are finished by re-reading the row (tsm_select.h), which is exact
+// and slower.
+#include "tsm_sample.h"
+#include "tsm_select.h"
+
+namespace tsm {
+
+enum : uint32_t {
+    ROWF_BUF_OVERFLOW = 1u,  // the buffer could not hold the candidates: re-read the row
+    ROWF_SLOW_HISTORY = 2u,  // history beyond the LDS table: penalties only on re-read
+};
+constexpr uint32_t kPruneAt = 3072;          // buffer fill that triggers an exact prune
+constexpr uint32_t kEntPen = 0x80000000u;    // buffer entry flags (ids < 2^22)
+constexpr uint32_t kEntAllowed = 0x40000000u;
+constexpr uint32_t kEntId = 0x003FFFFFu;
+static_assert(kVec == 2, "one group of 8 ids per thread and tile (tile_bounds)");
+static_assert(kBufCap % kBlock == 0, "compaction holds kBufCap / kBlock entries per thread");
+
+// Selection kinds over the buffer (and the penalized list).
+enum : uint32_t {
+    SK_ALL = 0,      // every buffer entry, canon(y)
+    SK_RAW = 1,      // non-penalized entries, canon(y) == canon(x); plus the penalized list, canon(x)
+    SK_ALLOWED = 2,  // allowed entries, total(y) (f32::total_cmp)
+};
+
+// Elements each target (SK_*) must keep: 0 = not tracked.
+struct Targets {
+    uint32_t need[3];
+};
+
+struct Sel3 {
+    uint64_t T[3];
+};
+
+__device__ __forceinline__ uint2* lds_buf() { return reinterpret_cast<uint2*>(lds_base() + kOffBuf); }
+__device__ __forceinline__ uint2* lds_pen() { return reinterpret_cast<uint2*>(lds_base() + kOffPen); }
+__device__ __forceinline__ uint32_t* lds_hist3() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHist); }
+__device__ __forceinline__ uint32_t* lds_misc() { return reinterpret_cast<uint32_t*>(lds_base() + kOffMisc); }
+__device__ __forceinline__ double* lds_miscd() { return reinterpret_cast<double*>(lds_base() + kOffMiscD); }
+__device__ __forceinline__ uint32_t* lds_tmp() { return reinterpret_cast<uint32_t*>(lds_base() + kOffTmp); }
+__device__ __forceinline__ uint32_t* lds_bitmap() { return reinterpret_cast<uint32_t*>(lds_base() + kOffBitmap); }
+__device__ __forceinline__ uint32_t* lds_hkey() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashKey); }
+__device__ __forceinline__ uint32_t* lds_hcnt() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashCnt); }
+
+// The running thresholds live in LDS (misc[M_THR + g], float bits) while a
+// prune or bound runs; the streaming loop keeps a register copy.
+__device__ __forceinline__ void load_thr(float thr[3]) {
+    const uint32_t* misc = lds_misc();
+#pragma unroll
+    for (int g = 0; g < 3; g++) thr[g] = __uint_as_float(misc[M_THR + g]);
+}
+
+// ---- history lookup -----------------------------------------------------------
+__device__ __forceinline__ uint32_t hash_slot(uint32_t id) { return (id * 2654435761u) >> 20; }  // 12 bits
+static_assert(kHashSlots == 4096, "hash_slot yields 12 bits");
+
+// Builds the bitmap of the row's history ids (< n) and their counts.  Needs
+// hlen <= kHistFast (the table then stays at most half full) and n <=
+// 32 * kBitmapWords.  Starts and ends with a barrier.
+__device__ void history_build(const uint32_t* hist, uint32_t hlen, uint32_t n) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t* bm = lds_bitmap();
+    uint32_t* hk = lds_hkey();
+    uint32_t* hc = lds_hcnt();
+    __syncthreads();
+    const uint32_t words = (n + 31) / 32;
+    for (uint32_t i = tid; i < words; i += kBlock) bm[i] = 0;
+    for (uint32_t i = tid; i < kHashSlots; i += kBlock) {
+        hk[i] = 0;
+        hc[i] = 0;
+    }
+    __syncthreads();
+    for (uint32_t h = tid; h < hlen; h += kBlock) {
+        const uint32_t id = hist[h];
+        if (id >= n) continue;  // ids past the vocabulary cap are ignored (sampler.rs:171)
+        atomicOr(&bm[id >> 5], 1u << (id & 31u));
+        uint32_t s = hash_slot(id);
+        for (uint32_t probe = 0; probe < kHashSlots; probe++) {
+            const uint32_t old = atomicCAS(&hk[s], 0u, id + 1u);
+            if (old == 0u || old == id + 1u) {
+                atomicAdd(&hc[s], 1u);
+                break;
+            }
+            s = (s + 1) & (kHashSlots - 1);
+        }
+    }
+    __syncthreads();
+}
+
+// Count of `id` in the history (its bitmap bit is set).
+__device__ __forceinline__ uint32_t history_count(uint32_t id) {
+    const uint32_t* hk = lds_hkey();
+    uint32_t s = hash_slot(id);
+    for (uint32_t probe = 0; probe < kHashSlots; probe++) {
+        const uint32_t k = hk[s];
+        if (k == id + 1u) return lds_hcnt()[s];
+        if (k == 0u) return 0u;
+        s = (s + 1) & (kHashSlots - 1);
+    }
+    return 0u;
+}
+
+// ---- buffer selections -----------------------------------------------------------
+__device__ __forceinline__ uint64_t entry_comp(uint32_t kind, uint2 e) {
+    const float y = __uint_as_float(e.x);
+    const uint32_t key = kind == SK_ALLOWED ? total_key(y) : canon_key(y);
+    return composite(key, e.y & kEntId);
+}
+
+__device__ __forceinline__ bool entry_in(uint32_t kind, uint2 e) {
+    return kind == SK_ALL || (kind == SK_RAW ? !(e.y & kEntPen) : (e.y & kEntAllowed) != 0);
+}
+
+// Three block-wide exclusive scans at once (two barriers).
+__device__ __forceinline__ void block_excl_scan3(const uint32_t v[3], uint32_t before[3], uint32_t total[3]) {
+    constexpr int NW = kBlock / kWave;
+    uint32_t* tmp = lds_tmp();
+    const uint32_t lane = lane_id(), wid = threadIdx.x / kWave;
+    uint32_t inc[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        inc[g] = wave_incl_scan(v[g]);
+        if (lane == kWave - 1) tmp[g * NW + wid] = inc[g];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        uint32_t b = 0, all = 0;
+        for (int w = 0; w < NW; w++) {
+            const uint32_t t = tmp[g * NW + w];
+            b += (w < static_cast<int>(wid)) ? t : 0u;
+            all += t;
+        }
+        before[g] = b + inc[g] - v[g];
+        total[g] = all;
+    }
+    __syncthreads();
+}
+
+// For up to three histograms (kBins bins each, ascending digit = best
+// first), finds the digit where the inclusive count reaches need[g] (> 0).
+// misc[M_SEL + 2g] = digit or ~0 (fewer than need), misc[M_SEL + 2g + 1] =
+// count before it.
+__device__ void hist_find3(const uint32_t need[3]) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t* h = lds_hist3();
+    uint32_t* res = lds_misc() + M_SEL;
+    static_assert(kBins == 2 * kBlock, "two bins per thread");
+    uint32_t c0[3], c1[3], s[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        c0[g] = need[g] ? h[g * kBins + 2 * t] : 0u;
+        c1[g] = need[g] ? h[g * kBins + 2 * t + 1] : 0u;
+        s[g] = c0[g] + c1[g];
+    }
+    if (t < 6) res[t] = (t & 1) ? 0u : 0xFFFFFFFFu;
+    uint32_t before[3], total[3];
+    block_excl_scan3(s, before, total);  // its barriers also order the res[] reset
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        const uint32_t nd = need[g];
+        if (nd && before[g] < nd && before[g] + s[g] >= nd) {
+            const bool first = before[g] + c0[g] >= nd;
+            res[2 * g] = first ? 2 * t : 2 * t + 1;
+            res[2 * g + 1] = first ? before[g] : before[g] + c0[g];
+        }
+    }
+    __syncthreads();
+}
+
+// Exact selection over the buffer (and, for SK_RAW with `with_pen`, the
+// penalized list): for each target g with need[g] > 0, the composite T[g]
+// such that exactly need[g] of its entries have composite <= T[g] (low bits
+// past the deciding digit are ones), or ~0 when it has fewer entries.
+// Radix rounds over the 54 live bits of the composite (~key << 32 | id),
+// stopping per target as soon as its digit's bin holds exactly what is left.
+__device__ __noinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool with_pen, Targets tg) {
+    const uint32_t tid = threadIdx.x;
+    const uint2* buf = lds_buf();
+    const uint2* pen = lds_pen();
+    uint32_t* h3 = lds_hist3();
+    const uint32_t* misc = lds_misc();
+    Sel3 out;
+    uint32_t need[3];
+    uint64_t known[3];
+    bool active[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        need[g] = tg.need[g];
+        known[g] = 0;
+        active[g] = need[g] > 0;
+        out.T[g] = ~0ull;
+    }
+    int known_lo = 64;
+    for (int r = 0; r < 5; r++) {
+        if (!(active[0] || active[1] || active[2])) break;
+        const int lo = r == 0 ? 53 : r == 1 ? 42 : r == 2 ? 32 : r == 3 ? 11 : 0;
+        const int w = r == 2 ? 10 : 11;
+        for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < bufn; i += kBlock) {
+            const uint2 e = buf[i];
+#pragma unroll
+            for (uint32_t g = 0; g < 3; g++) {
+                if (!active[g] || !entry_in(g, e)) continue;
+                const uint64_t c = entry_comp(g, e);
+                if (known_lo < 64 && (c >> known_lo) != (known[g] >> known_lo)) continue;
+                atomicAdd(&h3[g * kBins + ((c >> lo) & ((1u << w) - 1u))], 1u);
+            }
+        }
+        if (with_pen && active[SK_RAW]) {
+            for (uint32_t i = tid; i < penn; i += kBlock) {
+                const uint2 e = pen[i];
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                if (known_lo < 64 && (c >> known_lo) != (known[SK_RAW] >> known_lo)) continue;
+                atomicAdd(&h3[SK_RAW * kBins + ((c >> lo) & ((1u << w) - 1u))], 1u);
+            }
+        }
+        __syncthreads();
+        uint32_t nd[3];
+#pragma unroll
+        for (int g = 0; g < 3; g++) nd[g] = active[g] ? need[g] : 0u;
+        hist_find3(nd);
+        uint32_t d[3], before[3], inbin[3];
+#pragma unroll
+        for (int g = 0; g < 3; g++) {
+            d[g] = misc[M_SEL + 2 * g];
+            before[g] = misc[M_SEL + 2 * g + 1];
+            inbin[g] = (active[g] && d[g] != 0xFFFFFFFFu) ? h3[g * kBins + d[g]] : 0u;
+        }
+        __syncthreads();  // before the next round clears the histograms / rewrites M_SEL
+#pragma unroll
+        for (int g = 0; g < 3; g++) {
+            if (!active[g]) continue;
+            if (d[g] == 0xFFFFFFFFu) {  // fewer entries than need
+                active[g] = false;
+                continue;
+            }
+            known[g] |= static_cast<uint64_t>(d[g]) << lo;
+            need[g] -= before[g];
+            if (inbin[g] == need[g] || lo == 0) {
+                out.T[g] = lo == 0 ? known[g] : (known[g] | ((1ull << lo) - 1ull));
+                active[g] = false;
+            }
+        }
+        known_lo = lo;
+    }
+    return out;
+}
+
+// Value threshold of a selection result: every element whose key is at or
+// above the selected key prefix compares >= it as a float.
+__device__ __forceinline__ float comp_threshold(uint64_t T) {
+    const uint32_t key = ~static_cast<uint32_t>(T >> 32);
+    return key <= 0x007FFFFFu ? -INFINITY : key_to_float(key);
+}
+
+__device__ __forceinline__ bool keep_entry(const Targets& tg, const float thr[3], float y, bool pen, bool al) {
+    return (tg.need[SK_ALL] && y >= thr[SK_ALL]) || (tg.need[SK_RAW] && !pen && y >= thr[SK_RAW]) ||
+           (tg.need[SK_ALLOWED] && al && y >= thr[SK_ALLOWED]);
+}
+
+// Drops buffer entries below the thresholds in misc[M_THR] (order is not
+// kept); returns the new fill.
+__device__ __noinline__ uint32_t compact_buffer(Targets tg, uint32_t bufn) {
+    const uint32_t tid = threadIdx.x;
+    uint2* buf = lds_buf();
+    float thr[3];
+    load_thr(thr);
+    uint2 e[kBufCap / kBlock];
+    uint32_t mine = 0, keepmask = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kBufCap / kBlock; k++) {
+        const uint32_t i = tid + k * kBlock;
+        if (i < bufn) {
+            e[k] = buf[i];
+            if (keep_entry(tg, thr, __uint_as_float(e[k].x), (e[k].y & kEntPen) != 0, (e[k].y & kEntAllowed) != 0)) {
+                keepmask |= 1u << k;
+                mine++;
+            }
+        }
+    }
+    uint32_t total;
+    uint32_t pos = block_excl_scan<kBlock>(mine, lds_tmp(), &total);  // its barriers separate the reads above
+#pragma unroll
+    for (uint32_t k = 0; k < kBufCap / kBlock; k++)
+        if (keepmask & (1u << k)) buf[pos++] = e[k];
+    __syncthreads();
+    return total;
+}
+
+// Exact prune: raises each tracked threshold to its order statistic over the
+// buffer, then compacts; returns the new fill.
+__device__ __noinline__ uint32_t prune_buffer(Targets tg, uint32_t bufn) {
+    __syncthreads();  // the caller's buffer writes
+    const Sel3 s = buf_select(bufn, 0, false, tg);
+    uint32_t* misc = lds_misc();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int g = 0; g < 3; g++)
+            if (tg.need[g] && s.T[g] != ~0ull)
+                misc[M_THR + g] = __float_as_uint(fmaxf(__uint_as_float(misc[M_THR + g]), comp_threshold(s.T[g])));
+    }
+    __syncthreads();
+    return compact_buffer(tg, bufn);
+}
+
+// Lower bounds for the thresholds from one tile: k[g] is this thread's
+// largest key among its 8 ids relevant to target g (0: none).  For each
+// target, the digit (top 11 bits) of the need-th largest group maximum
+// gives a value with at least `need` of the tile's elements at or above it.
+__device__ __noinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t* h3 = lds_hist3();
+    uint32_t* misc = lds_misc();
+    for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
+    __syncthreads();
+    const uint32_t k[3] = {k0, k1, k2};
+#pragma unroll
+    for (int g = 0; g < 3; g++)
+        if (tg.need[g] && k[g] != 0u) atomicAdd(&h3[g * kBins + ((~k[g]) >> 21)], 1u);
+    __syncthreads();
+    hist_find3(tg.need);
+    if (tid == 0) {
+#pragma unroll
+        for (int g = 0; g < 3; g++) {
+            const uint32_t d = misc[M_SEL + 2 * g];
+            if (tg.need[g] && d != 0xFFFFFFFFu) {
+                const uint32_t key = ~((d << 21) | 0x1FFFFFu);
+                const float b = key <= 0x007FFFFFu ? -INFINITY : key_to_float(key);
+                misc[M_THR + g] = __float_as_uint(fmaxf(__uint_as_float(misc[M_THR + g]), b));
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <bool kVecLoads>
+__device__ __forceinline__ void load_tile(const float* rowp, const uint32_t* mrow, uint32_t tb, uint32_t n,
+                                          float (&v)[kVec][4], uint32_t (&mw)[kVec]) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < kVec; j++) {
+        const uint32_t id = tb + 4u * (j * kBlock + tid);
+        if (kVecLoads && id + 3 < n) {
+            const float4 f4 = *reinterpret_cast<const float4*>(rowp + id);
+            v[j][0] = f4.x;
+            v[j][1] = f4.y;
+            v[j][2] = f4.z;
+            v[j][3] = f4.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[j][q] = (id + q < n) ? rowp[id + q] : -INFINITY;
+        }
+        mw[j] = (mrow && id < n) ? mrow[id >> 5] : 0u;
+    }
+}
+
+// Emission mask of this thread's tile elements under the thresholds.
+__device__ __forceinline__ uint32_t emit_mask(const Targets& tg, const float thr[3], const float (&v)[kVec][4],
+                                              uint32_t valid_bits, uint32_t pen_bits, uint32_t al_bits) {
+    uint32_t emit = 0;
+#pragma unroll
+    for (int e = 0; e < kVec * 4; e++)
+        if (((valid_bits >> e) & 1u) && keep_entry(tg, thr, v[e >> 2][e & 3], (pen_bits >> e) & 1u, (al_bits >> e) & 1u))
+            emit |= 1u << e;
+    return emit;
+}
+
+// After the streaming pass: logsumexp and allowed count, then the pick (or
+// the distribution) and the logprobs of the row.
+__device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Targets tg0, const uint32_t nlp,
+                                           const float lmax, const double lsum, uint32_t nallow, uint32_t bufn) {
+    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+    const uint32_t n = f.n;
+    const RowMode m = f.m;
+    uint32_t* misc = lds_misc();
+    uint32_t* tmp = lds_tmp();
+    const uint2* buf = lds_buf();
+    const uint2* pen = lds_pen();
+
+    // ---------------- row statistics ----------------
+    __syncthreads();
+    float lse = 0.0f;
+    {
+        const uint32_t lane = lane_id(), wid = tid / kWave;
+        const float wm = wave_max(lmax);
+        double ws = (lmax != -INFINITY) ? lsum * exp(static_cast<double>(lmax) - static_cast<double>(wm)) : 0.0;
+        ws = wave_sum(ws);
+        const uint32_t wal = wave_sum(nallow);
+        float* wmax = reinterpret_cast<float*>(lds_miscd() + 8);  // 16 floats
+        double* wsum = lds_miscd() + 16;                           // 16 doubles
+        if (lane == 0) {
+            wmax[wid] = wm;
+            wsum[wid] = ws;
+            tmp[wid] = wal;
+        }
+        __syncthreads();
+        float rm = -INFINITY;
+        uint32_t al = 0;
+        for (int w = 0; w < kBlock / kWave; w++) {
+            rm = fmaxf(rm, wmax[w]);
+            al += tmp[w];
+        }
+        double rs = 0.0;
+        for (int w = 0; w < kBlock / kWave; w++)
+            if (wmax[w] != -INFINITY) rs += wsum[w] * exp(static_cast<double>(wmax[w]) - static_cast<double>(rm));
+        // sampler.rs:298-304: lse = max + (f32) ln(sum exp((f64)(l - max)))
+        lse = rm + static_cast<float>(log(rs));
+        nallow = al;
+        __syncthreads();
+    }
+    const uint32_t flags = misc[M_FLAGS];
+    const uint32_t penn = misc[M_PENN];
+    const bool buf_ok = !(flags & (ROWF_BUF_OVERFLOW | ROWF_SLOW_HISTORY));
+    const bool raw_ok = buf_ok && penn <= kPenCap;
+    __syncthreads();
+
+    // ---------------- finish ----------------
+    const float u = (a.uniforms && !a.distribution) ? a.uniforms[row] : 0.0f;
+    DistOut dist;
+    const DistOut* dptr = nullptr;
+    if (a.distribution) {
+        dist.ids = a.dist_ids + static_cast<size_t>(row) * a.dist_stride;
+        dist.probs = a.dist_probs + static_cast<size_t>(row) * a.dist_stride;
+        dist.stride = a.dist_stride;
+        dist.status = a.status;
+        dptr = &dist;
+    }
+    // exact selections over the buffer: the window, the fallback set, the raw top-n
+    Sel3 sel;
+    sel.T[0] = sel.T[1] = sel.T[2] = ~0ull;
+    if (buf_ok) {
+        Targets fin = tg0;
+        if (!raw_ok) fin.need[SK_RAW] = 0;
+        sel = buf_select(bufn, min(penn, kPenCap), true, fin);
+    }
+    Pick pk;
+    pk.token = 0;
+    pk.keep = 0;
+    pk.prob = 1.0f;
+    pk.mass = 0.0f;
+    if (m.constrained && nallow == 0) {
+        // nothing allowed: argmax of the raw row, no draw (sampler.rs:139-141)
+        if (raw_ok && sel.T[SK_RAW] != ~0ull) {
+            // the raw best is the smallest raw composite
+            unsigned long long best = ~0ull;
+            for (uint32_t i = tid; i < bufn; i += kBlock) {
+                const uint2 e = buf[i];
+                if (!(e.y & kEntPen)) {
+                    const uint64_t c = entry_comp(SK_ALL, e);
+                    best = c < best ? c : best;
+                }
+            }
+            for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
+                const uint2 e = pen[i];
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                best = c < best ? c : best;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long w = __shfl_xor(best, o, kWave);
+                best = w < best ? w : best;
+            }
+            unsigned long long* wb = reinterpret_cast<unsigned long long*>(lds_miscd() + 8);
+            if (lane_id() == 0) wb[tid / kWave] = best;
+            __syncthreads();
+            unsigned long long all = ~0ull;
+            for (int w = 0; w < kBlock / kWave; w++) all = wb[w] < all ? wb[w] : all;
+            __syncthreads();
+            pk.token = static_cast<uint32_t>(all);
+        } else {
+            Filt q;
+            q.order = ORD_CANON_X;
+            pk.token = static_cast<uint32_t>(exact_at(f, q, select_kth(f, q, 1)));
+        }
+    } else if (!m.topk) {
+        pk = reread_nucleus(f, nallow, u, dptr);
+    } else if (!buf_ok) {
+        const uint32_t len = reread_topk_list(f, nallow);
+        pk = finish_list(f, len, u, dptr);
+    } else {
+        // the ranked list from the buffer
+        uint64_t* gcomp = f.gcomp();
+        if (tid == 0) misc[M_CNT] = 0;
+        __syncthreads();
+        const bool constrained = m.constrained;
+        for (uint32_t i = tid; i < bufn; i += kBlock) {
+            const uint2 e = buf[i];
+            const uint64_t c = entry_comp(SK_ALL, e);
+            if (c <= sel.T[SK_ALL] && (!constrained || (e.y & kEntAllowed))) {
+                const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
+                if (pos < kExactCap) gcomp[pos] = c;
+            }
+        }
+        __syncthreads();
+        uint32_t g = min(misc[M_CNT], kExactCap);
+        __syncthreads();
+        uint32_t len = 0;
+        if (g > 0) {
+            sort_gathered(f, g);
+            len = min(g, m.want);
+        } else if (constrained) {
+            // no allowed id in the window: the whole-vocabulary fallback
+            // (sampler.rs:211-221), ordered by f32::total_cmp
+            if (tid == 0) misc[M_CNT] = 0;
+            __syncthreads();
+            for (uint32_t i = tid; i < bufn; i += kBlock) {
+                const uint2 e = buf[i];
+                if (!(e.y & kEntAllowed)) continue;
+                const uint64_t c = entry_comp(SK_ALLOWED, e);
+                if (c <= sel.T[SK_ALLOWED]) {
+                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
+                    if (pos < kExactCap) gcomp[pos] = c;
+                }
+            }
+            __syncthreads();
+            g = min(misc[M_CNT], kExactCap);
+            __syncthreads();
+            sort_gathered(f, g);
+            len = min(g, m.want);
+        }
+        pk = finish_list(f, len, u, dptr);
+    }
+
+    // ---------------- outputs ----------------
+    if (pk.token >= n) {  // a selection came back empty (e.g. NaN logits)
+        if (tid == 0) atomicOr(a.status, TSM_STATUS_INTERNAL);
+        pk.token = 0;
+    }
+    if (a.distribution) {
+        if (tid == 0) a.out_keep[row] = pk.keep;
+        return;
+    }
+    if (tid == 0) {
+        a.out_token[row] = pk.token;
+        if (a.out_prob) a.out_prob[row] = pk.prob;
+        if (a.out_keep) a.out_keep[row] = pk.keep;
+        if (m.logprobs && a.out_logprob) a.out_logprob[row] = f.rowp[pk.token] - lse;
+    }
+    if (nlp > 0) {
+        // raw top-n (sampler.rs:305-311): from the buffer's non-penalized
+        // entries and the penalized list, or by re-reading the row
+        uint64_t* gcomp = f.gcomp();
+        uint32_t nraw;
+        if (raw_ok && sel.T[SK_RAW] != ~0ull) {
+            if (tid == 0) misc[M_CNT] = 0;
+            __syncthreads();
+            for (uint32_t i = tid; i < bufn; i += kBlock) {
+                const uint2 e = buf[i];
+                if (e.y & kEntPen) continue;
+                const uint64_t c = entry_comp(SK_ALL, e);
+                if (c <= sel.T[SK_RAW]) {
+                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
+                    if (pos < kExactCap) gcomp[pos] = c;
+                }
+            }
+            for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
+                const uint2 e = pen[i];
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                if (c <= sel.T[SK_RAW]) {
+                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
+                    if (pos < kExactCap) gcomp[pos] = c;
+                }
+            }
+            __syncthreads();
+            const uint32_t g = min(misc[M_CNT], kExactCap);
+            __syncthreads();
+            sort_u64(gcomp, g);
+            nraw = min(g, nlp);
+        } else {
+            nraw = reread_raw_top(f, nlp);
+        }
+        if (tid < nraw) {
+            const uint64_t c = gcomp[tid];
+            const uint32_t id = static_cast<uint32_t>(c);
+            const float x = key_to_float(~static_cast<uint32_t>(c >> 32));
+            const size_t o = static_cast<size_t>(row) * a.top_stride + tid;
+            a.out_top_ids[o] = id;
+            if (a.out_top_lp) a.out_top_lp[o] = x - lse;
+        }
+    }
+}
+
+template <bool kVecLoads>
+__global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
+    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+    const uint32_t n = a.usable;
+    const tsm_row_params P = a.params[row];
+    uint32_t h0 = 0, hlen = 0;
+    if (a.hist_off) {
+        h0 = a.hist_off[row];
+        const uint32_t h1 = a.hist_off[row + 1];
+        hlen = h1 > h0 ? h1 - h0 : 0u;
+    }
+    Fin f;
+    f.rowp = a.logits + static_cast<size_t>(row) * a.row_stride;
+    f.hist = a.hist_ids ? a.hist_ids + h0 : nullptr;
+    f.hlen = hlen;
+    f.n = n;
+    // distribution() takes no constraint (sampler.rs:102-116)
+    f.m = row_mode(P, n, hlen, a.mask != nullptr && !a.distribution);
+    f.mrow = f.m.constrained ? a.mask + static_cast<size_t>(row) * a.mask_stride : nullptr;
+    f.P = P;
+    const RowMode m = f.m;  // register copies: f escapes to the re-read functions
+    const float* rowp = f.rowp;
+    const uint32_t* mrow = f.mrow;
+    uint32_t* misc = lds_misc();
+    uint2* buf = lds_buf();
+    uint2* pen = lds_pen();
+
+    uint32_t nlp = (m.logprobs && a.out_top_ids != nullptr) ? m.nlp : 0u;
+    if (nlp > a.top_stride) {  // the list must fit the row's slots
+        if (tid == 0) atomicOr(a.status, TSM_STATUS_BAD_PARAMS);
+        nlp = a.top_stride;
+    }
+    // penalties need the history lookup; without it the stream keeps no candidates
+    const bool fast_hist = !m.penal || (hlen <= kHistFast && n <= 32 * kBitmapWords);
+    Targets tg;
+    tg.need[SK_ALL] = (m.topk && fast_hist) ? m.window : 0u;
+    tg.need[SK_RAW] = fast_hist ? max(nlp, m.constrained ? 1u : 0u) : 0u;  // + raw argmax when nothing is allowed
+    tg.need[SK_ALLOWED] = (m.topk && m.constrained && fast_hist) ? m.want : 0u;
+    Targets tg0 = tg;
+    if (!fast_hist) tg0.need[SK_RAW] = max(nlp, m.constrained ? 1u : 0u);
+    const bool track_pen = tg.need[SK_RAW] > 0 && m.penal;
+
+    if (tid == 0) {
+        misc[M_PENN] = 0;
+        misc[M_FLAGS] = fast_hist ? 0u : ROWF_SLOW_HISTORY;
+        for (int g = 0; g < 3; g++) misc[M_THR + g] = __float_as_uint(-INFINITY);
+    }
+    if (m.penal && fast_hist) history_build(f.hist, hlen, n);  // barriers inside
+    float thr[3] = {-INFINITY, -INFINITY, -INFINITY};
+    const bool tracking = (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
+
+    // ---------------- streaming pass ----------------
+    float lmax = -INFINITY;  // raw max and sum exp(x - lmax) of this thread's ids
+    double lsum = 0.0;
+    uint32_t nallow = 0;
+    uint32_t bufn = 0;  // candidate buffer fill (uniform)
+    const uint32_t ntiles = (n + kTile - 1) / kTile;
+    float v[kVec][4], vn[kVec][4];
+    uint32_t mw[kVec], mwn[kVec];
+    load_tile<kVecLoads>(rowp, mrow, 0, n, v, mw);
+    for (uint32_t t = 0; t < ntiles; t++) {
+        const uint32_t tb = t * kTile;
+        const uint32_t tl = min(kTile, n - tb);
+        if (t + 1 < ntiles) load_tile<kVecLoads>(rowp, mrow, tb + kTile, n, vn, mwn);  // prefetch
+        uint32_t valid_bits = 0;
+#pragma unroll
+        for (int e = 0; e < kVec * 4; e++)
+            if (4u * ((e >> 2) * kBlock + tid) + (e & 3) < tl) valid_bits |= 1u << e;
+        // logsumexp partials of the raw logits
+        if (m.logprobs) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++)
+                if ((valid_bits >> e) & 1u) tmax = fmaxf(tmax, v[e >> 2][e & 3]);
+            if (tmax != -INFINITY) {
+                if (tmax > lmax) {
+                    if (lmax != -INFINITY) lsum *= exp(static_cast<double>(lmax) - static_cast<double>(tmax));
+                    lmax = tmax;
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < kVec * 4; e++)
+                    if ((valid_bits >> e) & 1u)
+                        sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lmax) * 1.44269504088896341f);
+                lsum += static_cast<double>(sum);
+            }
+        }
+        // penalties (v becomes the penalized y) and flags
+        uint32_t pen_bits = 0, al_bits = 0;
+#pragma unroll
+        for (int j = 0; j < kVec; j++) {
+            const uint32_t id0 = tb + 4u * (j * kBlock + tid);
+            if (m.penal && fast_hist && id0 < n) {
+                const uint32_t bits4 = (lds_bitmap()[id0 >> 5] >> (id0 & 31u)) & 0xFu;  // 4 ids of one word
+                if (bits4) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if (((bits4 >> q) & 1u) && id0 + q < n) {
+                            const float x = v[j][q];
+                            v[j][q] = penalize(x, history_count(id0 + q), m, P);
+                            pen_bits |= 1u << (j * 4 + q);
+                            if (track_pen) {
+                                const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
+                                if (pos < kPenCap) pen[pos] = make_uint2(__float_as_uint(x), id0 + q);
+                            }
+                        }
+                    }
+                }
+            }
+            if (m.constrained) al_bits |= ((mw[j] >> (id0 & 31u)) & 0xFu) << (j * 4);
+        }
+        al_bits &= valid_bits;
+        nallow += __popc(al_bits);
+        // candidates at or above the thresholds
+        if (tracking) {
+            uint32_t emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
+            uint32_t total;
+            uint32_t pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+            if (bufn + total > kBufCap) {
+                // too many: prune the buffer exactly, then fall back on the
+                // tile's group-max bounds, then give up on the buffer
+                if (bufn > 0) {
+                    bufn = prune_buffer(tg, bufn);
+                    load_thr(thr);
+                    emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
+                    pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+                }
+                if (bufn + total > kBufCap) {
+                    uint32_t k[3] = {0u, 0u, 0u};
+#pragma unroll
+                    for (int e = 0; e < kVec * 4; e++) {
+                        if (!((valid_bits >> e) & 1u)) continue;
+                        const float y = v[e >> 2][e & 3];
+                        k[SK_ALL] = max(k[SK_ALL], canon_key(y));
+                        if (!((pen_bits >> e) & 1u)) k[SK_RAW] = max(k[SK_RAW], canon_key(y));
+                        if ((al_bits >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
+                    }
+                    tile_bounds(tg, k[0], k[1], k[2]);
+                    bufn = compact_buffer(tg, bufn);
+                    load_thr(thr);
+                    emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
+                    pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+                }
+                if (bufn + total > kBufCap) {  // uniform: stop tracking, the finish re-reads
+                    if (tid == 0) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
+                    tg.need[SK_ALL] = tg.need[SK_RAW] = tg.need[SK_ALLOWED] = 0;
+                    emit = 0;
+                    total = 0;
+                }
+            }
+            uint32_t pos = bufn + pos0;
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++)
+                if ((emit >> e) & 1u) {
+                    const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
+                    buf[pos++] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
+                                            id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
+                                                (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
+                }
+            bufn += total;
+            if (bufn > kPruneAt) {
+                bufn = prune_buffer(tg, bufn);
+                load_thr(thr);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kVec; j++) {
+            mw[j] = mwn[j];
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[j][q] = vn[j][q];
+        }
+    }
+    finish_row(a, f, tg0, nlp, lmax, lsum, nallow, bufn);
+}
+
+template __global__ void sample_kernel<true>(SampleArgs);
+template __global__ void sample_kernel<false>(SampleArgs);
+
+void launch_sample(const SampleArgs& a, uint32_t rows, bool vec_loads, hipStream_t stream) {
+    if (vec_loads)
+        hipLaunchKernelGGL(sample_kernel<true>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+    else
+        hipLaunchKernelGGL(sample_kernel<false>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+}
+
+hipError_t sample_set_smem_attr() {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_kernel<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmem));
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_kernel<false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmem));
+    return e;
+}
+
+}  // namespace tsm

@@ -31,12 +31,15 @@
 #define __device__
 #define __host__
 #define __forceinline__ inline
+#define __noinline__ __attribute__((noinline))
 #define __launch_bounds__(...)
 #define __shared__ static
 #define __constant__ static
 #define __align__(n) alignas(n)
 #define HIP_DYNAMIC_SHARED(type, var) type* var = reinterpret_cast<type*>(::emu::dyn_smem());
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
+#define __builtin_amdgcn_readlane(v, l) emu_shfl((v), (l))
+#define __builtin_amdgcn_wave_barrier() ::emu::wave_sync()
 #define HIP_SYMBOL(x) (&(x))
 
 struct dim3 {

@@ -20,7 +20,12 @@ DRIVER = os.path.join(EMU_DIR, "emu_driver")
 
 
 def build(target="emu_driver"):
-    subprocess.run(["make", "-s", "-C", EMU_DIR, target], check=True)
+    """make under an exclusive lock (pytest-xdist workers build concurrently)."""
+    import fcntl
+
+    with open(os.path.join(EMU_DIR, ".build.lock"), "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        subprocess.run(["make", "-s", "-C", EMU_DIR, target], check=True)
     return os.path.join(EMU_DIR, target)
 
 
