@@ -6,7 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/tachyon_sampler.h"
+#include "tachyon_sampler.h"
 
 namespace tsm {
 
@@ -165,14 +165,22 @@ __device__ __forceinline__ uint32_t wave_min(uint32_t v) {
     }
     return v;
 }
+// Inclusive prefix sum over the wave with DPP row shifts and row broadcasts
+// (row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast 15 and 31
+// carry the row totals across rows); no LDS traffic.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        uint32_t w = __shfl_up(v, o, kWave);
-        if (lane >= o) v += w;
-    }
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));
     return v;
+}
+
+// Value of `v` in lane `lane` (uniform), as a scalar broadcast.
+__device__ __forceinline__ uint32_t wave_read(uint32_t v, uint32_t lane) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(lane)));
 }
 
 // Exclusive prefix sum over the block; `tmp` holds >= nwaves+1 words of LDS.

@@ -38,7 +38,8 @@ enum : uint32_t {
     ROWF_BUF_OVERFLOW = 1u,  // the buffer could not hold the candidates: re-read the row
     ROWF_SLOW_HISTORY = 2u,  // history beyond the LDS table: penalties only on re-read
 };
-constexpr uint32_t kPruneAt = 3072;          // buffer fill that triggers an exact prune
+constexpr uint32_t kPruneAt = 2048;          // fill at a sync point that triggers an exact prune
+                                             // (the rest is headroom for the next two tiles)
 constexpr uint32_t kEntPen = 0x80000000u;    // buffer entry flags (ids < 2^22)
 constexpr uint32_t kEntAllowed = 0x40000000u;
 constexpr uint32_t kEntId = 0x003FFFFFu;
@@ -197,13 +198,52 @@ __device__ void hist_find3(const uint32_t need[3]) {
     __syncthreads();
 }
 
+// Block-wide min and max of up to three u64 values per thread (one barrier
+// pair).  Empty inputs are min = ~0, max = 0.
+__device__ __forceinline__ void block_minmax3(unsigned long long mn[3], unsigned long long mx[3]) {
+    constexpr int NW = kBlock / kWave;
+    unsigned long long* t = reinterpret_cast<unsigned long long*>(lds_base() + kOffHist);  // 96 u64
+    const uint32_t lane = lane_id(), wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const unsigned long long a = __shfl_xor(mn[g], o, kWave), b = __shfl_xor(mx[g], o, kWave);
+            mn[g] = a < mn[g] ? a : mn[g];
+            mx[g] = b > mx[g] ? b : mx[g];
+        }
+        if (lane == 0) {
+            t[(2 * g) * NW + wid] = mn[g];
+            t[(2 * g + 1) * NW + wid] = mx[g];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        unsigned long long a = ~0ull, b = 0;
+        for (int w = 0; w < NW; w++) {
+            const unsigned long long x = t[(2 * g) * NW + w], y = t[(2 * g + 1) * NW + w];
+            a = x < a ? x : a;
+            b = y > b ? y : b;
+        }
+        mn[g] = a;
+        mx[g] = b;
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int high_bit64(unsigned long long v) { return v ? 63 - __builtin_clzll(v) : -1; }
+
 // Exact selection over the buffer (and, for SK_RAW with `with_pen`, the
 // penalized list): for each target g with need[g] > 0, the composite T[g]
 // such that exactly need[g] of its entries have composite <= T[g] (low bits
 // past the deciding digit are ones), or ~0 when it has fewer entries.
-// Radix rounds over the 54 live bits of the composite (~key << 32 | id),
-// stopping per target as soon as its digit's bin holds exactly what is left.
-__device__ __noinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool with_pen, Targets tg) {
+// Radix rounds of up to 11 bits over the composite (~key << 32 | id) start,
+// per target, at the highest bit where its entries differ (so the digits
+// spread over the bins instead of piling into a few) and skip bits 22..31,
+// which are zero in every composite; a target stops as soon as its digit's
+// bin holds exactly what is left.
+__device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool with_pen, Targets tg) {
     const uint32_t tid = threadIdx.x;
     const uint2* buf = lds_buf();
     const uint2* pen = lds_pen();
@@ -211,20 +251,49 @@ __device__ __noinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool with_
     const uint32_t* misc = lds_misc();
     Sel3 out;
     uint32_t need[3];
-    uint64_t known[3];
+    unsigned long long known[3];
+    int top[3];  // bits >= top are fixed (known); the next digit ends there
     bool active[3];
+    {
+        unsigned long long mn[3] = {~0ull, ~0ull, ~0ull}, mx[3] = {0ull, 0ull, 0ull};
+        for (uint32_t i = tid; i < bufn; i += kBlock) {
+            const uint2 e = buf[i];
 #pragma unroll
-    for (int g = 0; g < 3; g++) {
-        need[g] = tg.need[g];
-        known[g] = 0;
-        active[g] = need[g] > 0;
-        out.T[g] = ~0ull;
+            for (uint32_t g = 0; g < 3; g++) {
+                if (!tg.need[g] || !entry_in(g, e)) continue;
+                const unsigned long long c = entry_comp(g, e);
+                mn[g] = c < mn[g] ? c : mn[g];
+                mx[g] = c > mx[g] ? c : mx[g];
+            }
+        }
+        if (with_pen && tg.need[SK_RAW]) {
+            for (uint32_t i = tid; i < penn; i += kBlock) {
+                const uint2 e = pen[i];
+                const unsigned long long c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                mn[SK_RAW] = c < mn[SK_RAW] ? c : mn[SK_RAW];
+                mx[SK_RAW] = c > mx[SK_RAW] ? c : mx[SK_RAW];
+            }
+        }
+        block_minmax3(mn, mx);
+#pragma unroll
+        for (int g = 0; g < 3; g++) {
+            need[g] = tg.need[g];
+            out.T[g] = ~0ull;
+            active[g] = need[g] > 0 && mn[g] <= mx[g];  // something to select from
+            const int hb = high_bit64(mn[g] ^ mx[g]);
+            top[g] = hb + 1;  // 0: every entry has the same composite (one entry)
+            known[g] = hb < 0 ? mn[g] : hb >= 63 ? 0ull : (mn[g] & ~((2ull << hb) - 1ull));
+            if (active[g] && top[g] == 0) {  // a single entry
+                if (need[g] == 1) out.T[g] = mn[g];
+                active[g] = false;
+            }
+        }
     }
-    int known_lo = 64;
-    for (int r = 0; r < 5; r++) {
+    for (int r = 0; r < 6; r++) {
         if (!(active[0] || active[1] || active[2])) break;
-        const int lo = r == 0 ? 53 : r == 1 ? 42 : r == 2 ? 32 : r == 3 ? 11 : 0;
-        const int w = r == 2 ? 10 : 11;
+        int lo[3];
+#pragma unroll
+        for (int g = 0; g < 3; g++) lo[g] = top[g] > 11 ? top[g] - 11 : 0;
         for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
         __syncthreads();
         for (uint32_t i = tid; i < bufn; i += kBlock) {
@@ -232,17 +301,19 @@ __device__ __noinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool with_
 #pragma unroll
             for (uint32_t g = 0; g < 3; g++) {
                 if (!active[g] || !entry_in(g, e)) continue;
-                const uint64_t c = entry_comp(g, e);
-                if (known_lo < 64 && (c >> known_lo) != (known[g] >> known_lo)) continue;
-                atomicAdd(&h3[g * kBins + ((c >> lo) & ((1u << w) - 1u))], 1u);
+                const unsigned long long c = entry_comp(g, e);
+                if (top[g] < 64 && (c >> top[g]) != (known[g] >> top[g])) continue;
+                atomicAdd(&h3[g * kBins + static_cast<uint32_t>((c >> lo[g]) & ((1ull << (top[g] - lo[g])) - 1ull))],
+                          1u);
             }
         }
         if (with_pen && active[SK_RAW]) {
+            const int t1 = top[SK_RAW], l1 = lo[SK_RAW];
             for (uint32_t i = tid; i < penn; i += kBlock) {
                 const uint2 e = pen[i];
-                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
-                if (known_lo < 64 && (c >> known_lo) != (known[SK_RAW] >> known_lo)) continue;
-                atomicAdd(&h3[SK_RAW * kBins + ((c >> lo) & ((1u << w) - 1u))], 1u);
+                const unsigned long long c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                if (t1 < 64 && (c >> t1) != (known[SK_RAW] >> t1)) continue;
+                atomicAdd(&h3[SK_RAW * kBins + static_cast<uint32_t>((c >> l1) & ((1ull << (t1 - l1)) - 1ull))], 1u);
             }
         }
         __syncthreads();
@@ -265,14 +336,15 @@ __device__ __noinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool with_
                 active[g] = false;
                 continue;
             }
-            known[g] |= static_cast<uint64_t>(d[g]) << lo;
+            known[g] |= static_cast<unsigned long long>(d[g]) << lo[g];
             need[g] -= before[g];
-            if (inbin[g] == need[g] || lo == 0) {
-                out.T[g] = lo == 0 ? known[g] : (known[g] | ((1ull << lo) - 1ull));
+            if (inbin[g] == need[g] || lo[g] == 0) {
+                out.T[g] = lo[g] == 0 ? known[g] : (known[g] | ((1ull << lo[g]) - 1ull));
                 active[g] = false;
             }
+            top[g] = lo[g];
+            if (top[g] > 22 && top[g] <= 32) top[g] = 22;  // bits 22..31 of a composite are zero
         }
-        known_lo = lo;
     }
     return out;
 }
@@ -291,7 +363,7 @@ __device__ __forceinline__ bool keep_entry(const Targets& tg, const float thr[3]
 
 // Drops buffer entries below the thresholds in misc[M_THR] (order is not
 // kept); returns the new fill.
-__device__ __noinline__ uint32_t compact_buffer(Targets tg, uint32_t bufn) {
+__device__ __forceinline__ uint32_t compact_buffer(Targets tg, uint32_t bufn) {
     const uint32_t tid = threadIdx.x;
     uint2* buf = lds_buf();
     float thr[3];
@@ -320,7 +392,7 @@ __device__ __noinline__ uint32_t compact_buffer(Targets tg, uint32_t bufn) {
 
 // Exact prune: raises each tracked threshold to its order statistic over the
 // buffer, then compacts; returns the new fill.
-__device__ __noinline__ uint32_t prune_buffer(Targets tg, uint32_t bufn) {
+__device__ __forceinline__ uint32_t prune_buffer(Targets tg, uint32_t bufn) {
     __syncthreads();  // the caller's buffer writes
     const Sel3 s = buf_select(bufn, 0, false, tg);
     uint32_t* misc = lds_misc();
@@ -336,18 +408,33 @@ __device__ __noinline__ uint32_t prune_buffer(Targets tg, uint32_t bufn) {
 
 // Lower bounds for the thresholds from one tile: k[g] is this thread's
 // largest key among its 8 ids relevant to target g (0: none).  For each
-// target, the digit (top 11 bits) of the need-th largest group maximum
-// gives a value with at least `need` of the tile's elements at or above it.
-__device__ __noinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2) {
+// target the group maxima are histogrammed on the 11 bits below the prefix
+// they all share; the digit of the need-th largest gives a value with at
+// least `need` of the tile's elements at or above it.
+__device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2) {
     const uint32_t tid = threadIdx.x;
     uint32_t* h3 = lds_hist3();
     uint32_t* misc = lds_misc();
+    const uint32_t k[3] = {k0, k1, k2};
+    unsigned long long mn[3], mx[3];  // over ~key of the non-empty groups
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        mn[g] = (tg.need[g] && k[g]) ? static_cast<unsigned long long>(~k[g]) : ~0ull;
+        mx[g] = (tg.need[g] && k[g]) ? static_cast<unsigned long long>(~k[g]) : 0ull;
+    }
+    block_minmax3(mn, mx);
+    int lo[3], top[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        top[g] = mn[g] <= mx[g] ? high_bit64(mn[g] ^ mx[g]) + 1 : 0;
+        lo[g] = top[g] > 11 ? top[g] - 11 : 0;
+    }
     for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
     __syncthreads();
-    const uint32_t k[3] = {k0, k1, k2};
 #pragma unroll
     for (int g = 0; g < 3; g++)
-        if (tg.need[g] && k[g] != 0u) atomicAdd(&h3[g * kBins + ((~k[g]) >> 21)], 1u);
+        if (tg.need[g] && k[g] != 0u)
+            atomicAdd(&h3[g * kBins + (((~k[g]) >> lo[g]) & ((1u << (top[g] - lo[g])) - 1u))], 1u);
     __syncthreads();
     hist_find3(tg.need);
     if (tid == 0) {
@@ -355,7 +442,10 @@ __device__ __noinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, u
         for (int g = 0; g < 3; g++) {
             const uint32_t d = misc[M_SEL + 2 * g];
             if (tg.need[g] && d != 0xFFFFFFFFu) {
-                const uint32_t key = ~((d << 21) | 0x1FFFFFu);
+                // the bin's largest ~key (its lowest key): shared prefix, digit, ones below
+                const uint32_t pre = top[g] >= 32 ? 0u : (static_cast<uint32_t>(mn[g]) >> top[g]) << top[g];
+                const uint32_t nk = pre | (d << lo[g]) | ((1u << lo[g]) - 1u);
+                const uint32_t key = ~nk;
                 const float b = key <= 0x007FFFFFu ? -INFINITY : key_to_float(key);
                 misc[M_THR + g] = __float_as_uint(fmaxf(__uint_as_float(misc[M_THR + g]), b));
             }
@@ -399,7 +489,7 @@ __device__ __forceinline__ uint32_t emit_mask(const Targets& tg, const float thr
 // After the streaming pass: logsumexp and allowed count, then the pick (or
 // the distribution) and the logprobs of the row.
 __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Targets tg0, const uint32_t nlp,
-                                           const float lmax, const double lsum, uint32_t nallow, uint32_t bufn) {
+                                           const float lref, const double lsum, uint32_t nallow, uint32_t bufn) {
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const uint32_t n = f.n;
     const RowMode m = f.m;
@@ -410,40 +500,72 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
 
     // ---------------- row statistics ----------------
     __syncthreads();
-    float lse = 0.0f;
     {
-        const uint32_t lane = lane_id(), wid = tid / kWave;
-        const float wm = wave_max(lmax);
-        double ws = (lmax != -INFINITY) ? lsum * exp(static_cast<double>(lmax) - static_cast<double>(wm)) : 0.0;
-        ws = wave_sum(ws);
         const uint32_t wal = wave_sum(nallow);
-        float* wmax = reinterpret_cast<float*>(lds_miscd() + 8);  // 16 floats
-        double* wsum = lds_miscd() + 16;                           // 16 doubles
-        if (lane == 0) {
-            wmax[wid] = wm;
-            wsum[wid] = ws;
-            tmp[wid] = wal;
-        }
+        if (lane_id() == 0) tmp[tid / kWave] = wal;
         __syncthreads();
-        float rm = -INFINITY;
         uint32_t al = 0;
-        for (int w = 0; w < kBlock / kWave; w++) {
-            rm = fmaxf(rm, wmax[w]);
-            al += tmp[w];
-        }
-        double rs = 0.0;
-        for (int w = 0; w < kBlock / kWave; w++)
-            if (wmax[w] != -INFINITY) rs += wsum[w] * exp(static_cast<double>(wmax[w]) - static_cast<double>(rm));
-        // sampler.rs:298-304: lse = max + (f32) ln(sum exp((f64)(l - max)))
-        lse = rm + static_cast<float>(log(rs));
+        for (int w = 0; w < kBlock / kWave; w++) al += tmp[w];
         nallow = al;
         __syncthreads();
     }
     const uint32_t flags = misc[M_FLAGS];
     const uint32_t penn = misc[M_PENN];
     const bool buf_ok = !(flags & (ROWF_BUF_OVERFLOW | ROWF_SLOW_HISTORY));
-    const bool raw_ok = buf_ok && penn <= kPenCap;
+    const bool raw_ok = buf_ok && penn <= kPenCap && tg0.need[SK_RAW] > 0;
     __syncthreads();
+    // the best raw logit (value desc, id asc): the raw argmax and the max of
+    // the logsumexp, from the buffer's non-penalized entries and the
+    // penalized list, or by re-reading the row
+    uint64_t raw_best = ~0ull;
+    const bool none_allowed = m.constrained && nallow == 0;
+    if (m.logprobs || none_allowed) {
+        if (raw_ok) {
+            unsigned long long best = ~0ull;
+            for (uint32_t i = tid; i < bufn; i += kBlock) {
+                const uint2 e = buf[i];
+                if (!(e.y & kEntPen)) {
+                    const uint64_t c = entry_comp(SK_ALL, e);
+                    best = c < best ? c : best;
+                }
+            }
+            for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
+                const uint2 e = pen[i];
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                best = c < best ? c : best;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long w = __shfl_xor(best, o, kWave);
+                best = w < best ? w : best;
+            }
+            unsigned long long* wb = reinterpret_cast<unsigned long long*>(lds_miscd() + 8);
+            if (lane_id() == 0) wb[tid / kWave] = best;
+            __syncthreads();
+            unsigned long long all = ~0ull;
+            for (int w = 0; w < kBlock / kWave; w++) all = wb[w] < all ? wb[w] : all;
+            __syncthreads();
+            raw_best = all;
+        } else {
+            Filt q;
+            q.order = ORD_CANON_X;
+            raw_best = exact_at(f, q, select_kth(f, q, 1));
+        }
+    }
+    float lse = 0.0f;
+    if (m.logprobs) {
+        // sampler.rs:298-304: lse = max + (f32) ln(sum exp((f64)(l - max)))
+        const float rmax = key_to_float(~static_cast<uint32_t>(raw_best >> 32));
+        double part = lsum * exp(static_cast<double>(lref) - static_cast<double>(rmax));
+        part = wave_sum(part);
+        double* wsum = lds_miscd() + 16;  // 16 doubles
+        if (lane_id() == 0) wsum[tid / kWave] = part;
+        __syncthreads();
+        double rs = 0.0;
+        for (int w = 0; w < kBlock / kWave; w++) rs += wsum[w];
+        lse = rmax + static_cast<float>(log(rs));
+        __syncthreads();
+    }
 
     // ---------------- finish ----------------
     const float u = (a.uniforms && !a.distribution) ? a.uniforms[row] : 0.0f;
@@ -469,40 +591,9 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
     pk.keep = 0;
     pk.prob = 1.0f;
     pk.mass = 0.0f;
-    if (m.constrained && nallow == 0) {
+    if (none_allowed) {
         // nothing allowed: argmax of the raw row, no draw (sampler.rs:139-141)
-        if (raw_ok && sel.T[SK_RAW] != ~0ull) {
-            // the raw best is the smallest raw composite
-            unsigned long long best = ~0ull;
-            for (uint32_t i = tid; i < bufn; i += kBlock) {
-                const uint2 e = buf[i];
-                if (!(e.y & kEntPen)) {
-                    const uint64_t c = entry_comp(SK_ALL, e);
-                    best = c < best ? c : best;
-                }
-            }
-            for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
-                const uint2 e = pen[i];
-                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
-                best = c < best ? c : best;
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const unsigned long long w = __shfl_xor(best, o, kWave);
-                best = w < best ? w : best;
-            }
-            unsigned long long* wb = reinterpret_cast<unsigned long long*>(lds_miscd() + 8);
-            if (lane_id() == 0) wb[tid / kWave] = best;
-            __syncthreads();
-            unsigned long long all = ~0ull;
-            for (int w = 0; w < kBlock / kWave; w++) all = wb[w] < all ? wb[w] : all;
-            __syncthreads();
-            pk.token = static_cast<uint32_t>(all);
-        } else {
-            Filt q;
-            q.order = ORD_CANON_X;
-            pk.token = static_cast<uint32_t>(exact_at(f, q, select_kth(f, q, 1)));
-        }
+        pk.token = static_cast<uint32_t>(raw_best);
     } else if (!m.topk) {
         pk = reread_nucleus(f, nallow, u, dptr);
     } else if (!buf_ok) {
@@ -647,56 +738,71 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     const bool fast_hist = !m.penal || (hlen <= kHistFast && n <= 32 * kBitmapWords);
     Targets tg;
     tg.need[SK_ALL] = (m.topk && fast_hist) ? m.window : 0u;
-    tg.need[SK_RAW] = fast_hist ? max(nlp, m.constrained ? 1u : 0u) : 0u;  // + raw argmax when nothing is allowed
+    // the raw top-n, and the raw best for the logsumexp / the argmax when nothing is allowed
+    tg.need[SK_RAW] = fast_hist ? max(nlp, (m.constrained || m.logprobs) ? 1u : 0u) : 0u;
     tg.need[SK_ALLOWED] = (m.topk && m.constrained && fast_hist) ? m.want : 0u;
     Targets tg0 = tg;
-    if (!fast_hist) tg0.need[SK_RAW] = max(nlp, m.constrained ? 1u : 0u);
+    if (!fast_hist) tg0.need[SK_RAW] = 0u;
     const bool track_pen = tg.need[SK_RAW] > 0 && m.penal;
 
     if (tid == 0) {
+        misc[M_BUFN] = 0;
         misc[M_PENN] = 0;
         misc[M_FLAGS] = fast_hist ? 0u : ROWF_SLOW_HISTORY;
         for (int g = 0; g < 3; g++) misc[M_THR + g] = __float_as_uint(-INFINITY);
     }
+    // tiles t+1 and t+2 are in flight while tile t is processed
+    float v[kVec][4], vn[kVec][4], vn2[kVec][4];
+    uint32_t mw[kVec], mwn[kVec], mwn2[kVec];
+    load_tile<kVecLoads>(rowp, mrow, 0, n, v, mw);             // in flight while the lookup is built
+    if (kTile < n) load_tile<kVecLoads>(rowp, mrow, kTile, n, vn, mwn);
     if (m.penal && fast_hist) history_build(f.hist, hlen, n);  // barriers inside
     float thr[3] = {-INFINITY, -INFINITY, -INFINITY};
     const bool tracking = (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
 
     // ---------------- streaming pass ----------------
-    float lmax = -INFINITY;  // raw max and sum exp(x - lmax) of this thread's ids
-    double lsum = 0.0;
+    double lsum = 0.0;  // sum of exp(x - lref) over this thread's ids
+    float lref = 0.0f;
+    if (m.logprobs) {
+        float t0 = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < kVec * 4; e++) t0 = fmaxf(t0, v[e >> 2][e & 3]);
+        lref = t0 == -INFINITY ? 0.0f : t0;
+    }
     uint32_t nallow = 0;
     uint32_t bufn = 0;  // candidate buffer fill (uniform)
     const uint32_t ntiles = (n + kTile - 1) / kTile;
-    float v[kVec][4], vn[kVec][4];
-    uint32_t mw[kVec], mwn[kVec];
-    load_tile<kVecLoads>(rowp, mrow, 0, n, v, mw);
     for (uint32_t t = 0; t < ntiles; t++) {
         const uint32_t tb = t * kTile;
         const uint32_t tl = min(kTile, n - tb);
-        if (t + 1 < ntiles) load_tile<kVecLoads>(rowp, mrow, tb + kTile, n, vn, mwn);  // prefetch
-        uint32_t valid_bits = 0;
-#pragma unroll
-        for (int e = 0; e < kVec * 4; e++)
-            if (4u * ((e >> 2) * kBlock + tid) + (e & 3) < tl) valid_bits |= 1u << e;
-        // logsumexp partials of the raw logits
-        if (m.logprobs) {
-            float tmax = -INFINITY;
+        if (t + 2 < ntiles) load_tile<kVecLoads>(rowp, mrow, tb + 2 * kTile, n, vn2, mwn2);  // prefetch
+        uint32_t valid_bits = (1u << (kVec * 4)) - 1u;
+        if (tl < kTile) {  // the row's last, partial tile
+            valid_bits = 0;
 #pragma unroll
             for (int e = 0; e < kVec * 4; e++)
-                if ((valid_bits >> e) & 1u) tmax = fmaxf(tmax, v[e >> 2][e & 3]);
-            if (tmax != -INFINITY) {
-                if (tmax > lmax) {
-                    if (lmax != -INFINITY) lsum *= exp(static_cast<double>(lmax) - static_cast<double>(tmax));
-                    lmax = tmax;
-                }
-                float sum = 0.0f;
+                if (4u * ((e >> 2) * kBlock + tid) + (e & 3) < tl) valid_bits |= 1u << e;
+        }
+        // logsumexp partials: sum of exp(x - ref) with a per-thread reference
+        // (ids past the row hold -inf and add 0); a tile whose terms grow past
+        // 2^100 moves the reference to its own maximum
+        if (m.logprobs) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++)
+                sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
+            if (!(sum < 0x1p100f)) {
+                float tmax = lref;
+#pragma unroll
+                for (int e = 0; e < kVec * 4; e++) tmax = fmaxf(tmax, v[e >> 2][e & 3]);
+                lsum *= exp2(static_cast<double>(lref - tmax) * 1.4426950408889634);
+                lref = tmax;
+                sum = 0.0f;
 #pragma unroll
                 for (int e = 0; e < kVec * 4; e++)
-                    if ((valid_bits >> e) & 1u)
-                        sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lmax) * 1.44269504088896341f);
-                lsum += static_cast<double>(sum);
+                    sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
             }
+            lsum += static_cast<double>(sum);
         }
         // penalties (v becomes the penalized y) and flags
         uint32_t pen_bits = 0, al_bits = 0;
@@ -727,18 +833,12 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         // candidates at or above the thresholds
         if (tracking) {
             uint32_t emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
-            uint32_t total;
-            uint32_t pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
-            if (bufn + total > kBufCap) {
-                // too many: prune the buffer exactly, then fall back on the
-                // tile's group-max bounds, then give up on the buffer
-                if (bufn > 0) {
-                    bufn = prune_buffer(tg, bufn);
-                    load_thr(thr);
-                    emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
-                    pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
-                }
-                if (bufn + total > kBufCap) {
+            if (t == 0) {
+                // first tile: block-wide, so the thresholds can start from the
+                // tile's own group-max bounds
+                uint32_t total;
+                uint32_t pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+                if (total > kBufCap) {
                     uint32_t k[3] = {0u, 0u, 0u};
 #pragma unroll
                     for (int e = 0; e < kVec * 4; e++) {
@@ -749,41 +849,82 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                         if ((al_bits >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
                     }
                     tile_bounds(tg, k[0], k[1], k[2]);
-                    bufn = compact_buffer(tg, bufn);
                     load_thr(thr);
                     emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
                     pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
                 }
-                if (bufn + total > kBufCap) {  // uniform: stop tracking, the finish re-reads
+                if (total > kBufCap) {  // uniform: stop tracking, the finish re-reads
                     if (tid == 0) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
                     tg.need[SK_ALL] = tg.need[SK_RAW] = tg.need[SK_ALLOWED] = 0;
                     emit = 0;
                     total = 0;
                 }
-            }
-            uint32_t pos = bufn + pos0;
+                uint32_t pos = pos0;
 #pragma unroll
-            for (int e = 0; e < kVec * 4; e++)
-                if ((emit >> e) & 1u) {
-                    const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
-                    buf[pos++] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
-                                            id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
-                                                (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
+                for (int e = 0; e < kVec * 4; e++)
+                    if ((emit >> e) & 1u) {
+                        const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
+                        buf[pos++] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
+                                                id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
+                                                    (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
+                    }
+                if (tid == 0) misc[M_BUFN] = total;
+                __syncthreads();
+            } else {
+                // later tiles: each wave reserves its slots with one LDS atomic,
+                // no barrier; a reservation past the buffer flags the row
+                const uint32_t cnt = __popc(emit);
+                const uint32_t incl = wave_incl_scan(cnt);
+                const uint32_t wtot = wave_read(incl, kWave - 1);
+                if (wtot) {
+                    uint32_t base = 0;
+                    if (lane_id() == kWave - 1) base = atomicAdd(&misc[M_BUFN], wtot);
+                    base = wave_read(base, kWave - 1);
+                    if (base + wtot <= kBufCap) {
+                        uint32_t pos = base + incl - cnt;
+#pragma unroll
+                        for (int e = 0; e < kVec * 4; e++)
+                            if ((emit >> e) & 1u) {
+                                const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
+                                buf[pos++] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
+                                                        id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
+                                                            (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
+                            }
+                    } else if (lane_id() == 0) {
+                        atomicOr(&misc[M_FLAGS], static_cast<uint32_t>(ROWF_BUF_OVERFLOW));
+                    }
                 }
-            bufn += total;
-            if (bufn > kPruneAt) {
-                bufn = prune_buffer(tg, bufn);
-                load_thr(thr);
+            }
+            // every second tile: a sync point that prunes a filling buffer
+            if ((t & 1u) == 1u && t + 1 < ntiles) {
+                __syncthreads();
+                const uint32_t fl = misc[M_FLAGS];
+                bufn = misc[M_BUFN];
+                __syncthreads();  // every wave has read the fill before anyone adds to it
+                if (fl & ROWF_BUF_OVERFLOW) {
+                    tg.need[SK_ALL] = tg.need[SK_RAW] = tg.need[SK_ALLOWED] = 0;  // uniform
+                } else if (bufn > kPruneAt) {
+                    bufn = prune_buffer(tg, bufn);
+                    if (tid == 0) misc[M_BUFN] = bufn;
+                    load_thr(thr);
+                    __syncthreads();
+                }
             }
         }
 #pragma unroll
         for (int j = 0; j < kVec; j++) {
             mw[j] = mwn[j];
+            mwn[j] = mwn2[j];
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[j][q] = vn[j][q];
+            for (int q = 0; q < 4; q++) {
+                v[j][q] = vn[j][q];
+                vn[j][q] = vn2[j][q];
+            }
         }
     }
-    finish_row(a, f, tg0, nlp, lmax, lsum, nallow, bufn);
+    __syncthreads();
+    bufn = tracking ? min(misc[M_BUFN], kBufCap) : 0u;
+    finish_row(a, f, tg0, nlp, lref, lsum, nallow, bufn);
 }
 
 template __global__ void sample_kernel<true>(SampleArgs);

@@ -39,6 +39,7 @@
 #define HIP_DYNAMIC_SHARED(type, var) type* var = reinterpret_cast<type*>(::emu::dyn_smem());
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_readlane(v, l) emu_shfl((v), (l))
+#define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((old), (src), (ctrl), (rm), (bm), (bc))
 #define __builtin_amdgcn_wave_barrier() ::emu::wave_sync()
 #define HIP_SYMBOL(x) (&(x))
 
@@ -114,6 +115,29 @@ inline T emu_shfl(T v, int src) {
     std::memcpy(&r, &got, sizeof(T));
     return r;
 }
+// DPP moves used by the kernels: row_shr:1..15 (0x111..0x11f) and the wave64
+// row broadcasts row_bcast:15 (0x142) and row_bcast:31 (0x143).
+inline int emu_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+    const int lane = ::emu::lane_id();
+    const int row = lane / 16, inrow = lane % 16;
+    int from = -1;
+    if (ctrl > 0x110 && ctrl <= 0x11f) {
+        const int n = ctrl - 0x110;
+        if (inrow >= n) from = lane - n;
+    } else if (ctrl == 0x142) {
+        if (row >= 1) from = (row - 1) * 16 + 15;
+    } else if (ctrl == 0x143) {
+        if (row >= 2) from = 31;
+    } else {
+        std::fprintf(stderr, "EMU: unsupported DPP control 0x%x\n", ctrl);
+        std::abort();
+    }
+    const int got = emu_shfl(src, from < 0 ? lane : from);  // every lane takes part
+    if (!((row_mask >> row) & 1) || !((bank_mask >> (inrow / 4)) & 1)) return old;
+    if (from < 0) return bound_ctrl ? 0 : old;
+    return got;
+}
+
 template <class T>
 inline T __shfl_xor(T v, int mask, int width = 64) {
     const int lane = ::emu::lane_id();
