@@ -14,7 +14,7 @@ namespace tsm {
 constexpr int kWave = 64;
 constexpr int kBlock = 1024;           // one workgroup (16 waves) per row
 constexpr int kVec = 2;                // float4 loads per thread per tile
-constexpr uint32_t kTile = kBlock * kVec * 4;  // 16384 ids per tile
+constexpr uint32_t kTile = kBlock * kVec * 4;  // 8192 ids per tile of the streaming pass
 constexpr uint32_t kMaxWindow = 1024;  // top_n path bound (sampler.rs:193)
 constexpr uint32_t kWideWindow = 256;  // constrained window floor (sampler.rs:186-187)
 constexpr uint32_t kExactCap = 1024;   // longest ranked list finished exactly
@@ -181,6 +181,21 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
 // Value of `v` in lane `lane` (uniform), as a scalar broadcast.
 __device__ __forceinline__ uint32_t wave_read(uint32_t v, uint32_t lane) {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(lane)));
+}
+// A value every active lane holds alike, moved to a scalar register.
+__device__ __forceinline__ uint32_t wave_uniform(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+// Mask of the lanes whose predicate holds (bit i = lane i).
+__device__ __forceinline__ uint64_t wave_ballot(bool p) { return static_cast<uint64_t>(__ballot(p)); }
+// Number of lanes below this one whose bit is set in `mask`.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+// Load of an LDS word that other waves update with atomics meanwhile.
+__device__ __forceinline__ uint32_t lds_load_relaxed(uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Exclusive prefix sum over the block; `tmp` holds >= nwaves+1 words of LDS.

@@ -17,9 +17,13 @@
 //     logprobs) and the best allowed values (the whole-vocabulary fallback
 //     of sampler.rs:211-221).  Penalized ids also go to a list with their
 //     raw values.  A threshold starts from a lower bound read off the first
-//     tile's group maxima and is raised to the exact order statistic
-//     whenever the buffer fills, so the buffer ends holding a small superset
-//     of every element the finish can need.
+//     tile's group maxima.  After that the waves never wait for each other:
+//     each wave reserves buffer slots with one LDS atomic, every kept
+//     element is also counted in a small per-threshold histogram of its key,
+//     and one wave per tile raises the thresholds (LDS atomicMax) to the
+//     highest histogram edge with enough counted elements above it.  The
+//     buffer ends holding a small superset of every element the finish can
+//     need.
 // Finish: exact radix selects over the buffer give the window, the allowed
 // ids inside it (or the fallback set) and the raw top-n; the ranked list is
 // sorted and finished with the reference's own sequential f32 arithmetic
@@ -38,13 +42,13 @@ enum : uint32_t {
     ROWF_BUF_OVERFLOW = 1u,  // the buffer could not hold the candidates: re-read the row
     ROWF_SLOW_HISTORY = 2u,  // history beyond the LDS table: penalties only on re-read
 };
-constexpr uint32_t kPruneAt = 2048;          // fill at a sync point that triggers an exact prune
-                                             // (the rest is headroom for the next two tiles)
+constexpr uint32_t kKeyNegInf = 0x007FFFFFu;     // canon_key(-inf): a threshold every non-NaN value passes
+constexpr uint32_t kKeyUntracked = 0xFFFFFFFFu;  // threshold of a target not tracked: reads as NaN, keeps nothing
 constexpr uint32_t kEntPen = 0x80000000u;    // buffer entry flags (ids < 2^22)
 constexpr uint32_t kEntAllowed = 0x40000000u;
 constexpr uint32_t kEntId = 0x003FFFFFu;
 static_assert(kVec == 2, "one group of 8 ids per thread and tile (tile_bounds)");
-static_assert(kBufCap % kBlock == 0, "compaction holds kBufCap / kBlock entries per thread");
+static_assert(kSBins == 8 * kWave, "raise_thresholds reads 8 bins per lane");
 
 // Selection kinds over the buffer (and the penalized list).
 enum : uint32_t {
@@ -71,14 +75,12 @@ __device__ __forceinline__ uint32_t* lds_tmp() { return reinterpret_cast<uint32_
 __device__ __forceinline__ uint32_t* lds_bitmap() { return reinterpret_cast<uint32_t*>(lds_base() + kOffBitmap); }
 __device__ __forceinline__ uint32_t* lds_hkey() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashKey); }
 __device__ __forceinline__ uint32_t* lds_hcnt() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashCnt); }
+__device__ __forceinline__ uint32_t* lds_shist() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSHist); }
 
-// The running thresholds live in LDS (misc[M_THR + g], float bits) while a
-// prune or bound runs; the streaming loop keeps a register copy.
-__device__ __forceinline__ void load_thr(float thr[3]) {
-    const uint32_t* misc = lds_misc();
-#pragma unroll
-    for (int g = 0; g < 3; g++) thr[g] = __uint_as_float(misc[M_THR + g]);
-}
+// The running thresholds are canon keys in LDS (misc[M_THR + g]), raised
+// only by atomicMax.  As a float, y >= key_to_float(k) holds exactly when
+// canon_key(y) >= k for every non-NaN y; kKeyUntracked reads as NaN.
+__device__ __forceinline__ float thr_float(uint32_t k) { return key_to_float(k); }
 
 // ---- history lookup -----------------------------------------------------------
 __device__ __forceinline__ uint32_t hash_slot(uint32_t id) { return (id * 2654435761u) >> 20; }  // 12 bits
@@ -349,69 +351,82 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
     return out;
 }
 
-// Value threshold of a selection result: every element whose key is at or
-// above the selected key prefix compares >= it as a float.
-__device__ __forceinline__ float comp_threshold(uint64_t T) {
-    const uint32_t key = ~static_cast<uint32_t>(T >> 32);
-    return key <= 0x007FFFFFu ? -INFINITY : key_to_float(key);
+// Whether a (penalized) value y is kept by one of the three thresholds: the
+// raw one applies to non-penalized ids, the allowed one to allowed ids.
+// Branch-free; an untracked threshold is NaN and keeps nothing.
+__device__ __forceinline__ bool keep3(float y, bool pen, bool al, float tA, float tR, float tL) {
+    return static_cast<bool>((y >= tA) | (!pen & (y >= tR)) | (al & (y >= tL)));
 }
 
-__device__ __forceinline__ bool keep_entry(const Targets& tg, const float thr[3], float y, bool pen, bool al) {
-    return (tg.need[SK_ALL] && y >= thr[SK_ALL]) || (tg.need[SK_RAW] && !pen && y >= thr[SK_RAW]) ||
-           (tg.need[SK_ALLOWED] && al && y >= thr[SK_ALLOWED]);
-}
+// Geometry of the stream histograms: bin = (key - base) >> shift, clamped to
+// the last bin; base is a threshold's key after the first tile (every key a
+// threshold keeps afterwards is at or above it) and the shift puts the first
+// tile's largest key near the middle of the bins.
+struct SHist {
+    uint32_t base[3], shift[3];
+};
 
-// Drops buffer entries below the thresholds in misc[M_THR] (order is not
-// kept); returns the new fill.
-__device__ __forceinline__ uint32_t compact_buffer(Targets tg, uint32_t bufn) {
-    const uint32_t tid = threadIdx.x;
-    uint2* buf = lds_buf();
-    float thr[3];
-    load_thr(thr);
-    uint2 e[kBufCap / kBlock];
-    uint32_t mine = 0, keepmask = 0;
+// Counts a kept element in the histogram of each threshold that keeps it.
+__device__ __forceinline__ void count_kept(float y, bool pen, bool al, float tA, float tR, float tL, const SHist& h) {
+    uint32_t* sh = lds_shist();
+    const uint32_t key = canon_key(y);
+    const bool c[3] = {y >= tA, static_cast<bool>(!pen & (y >= tR)), static_cast<bool>(al & (y >= tL))};
 #pragma unroll
-    for (uint32_t k = 0; k < kBufCap / kBlock; k++) {
-        const uint32_t i = tid + k * kBlock;
-        if (i < bufn) {
-            e[k] = buf[i];
-            if (keep_entry(tg, thr, __uint_as_float(e[k].x), (e[k].y & kEntPen) != 0, (e[k].y & kEntAllowed) != 0)) {
-                keepmask |= 1u << k;
-                mine++;
+    for (int g = 0; g < 3; g++)
+        if (c[g] && key >= h.base[g]) atomicAdd(&sh[g * kSBins + min((key - h.base[g]) >> h.shift[g], kSBins - 1)], 1u);
+}
+
+// One wave raises each tracked threshold to the lower edge of the highest
+// histogram bin at which the counts, summed from the top bin down, reach
+// need[g]: that many kept elements have keys at or above the edge, so no
+// element below it can be among the target's best.  Other waves keep adding
+// to the counts meanwhile; counts only grow, so whatever mix of old and new
+// counts is read is still a valid lower bound.  A bin that holds an element
+// has its edge at or below that element's key, so the edge never wraps.
+__device__ __forceinline__ void raise_thresholds(const Targets& tg, const SHist& h) {
+    const uint32_t lane = lane_id();
+    uint32_t* misc = lds_misc();
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        const uint32_t need = tg.need[g];
+        if (!need) continue;
+        const uint32_t lo = kSBins - 8u * (lane + 1u);  // lane 0 holds the 8 top bins
+        uint32_t* bins = lds_shist() + g * kSBins + lo;
+        uint32_t c[8], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            c[i] = lds_load_relaxed(bins + i);
+            sum += c[i];
+        }
+        const uint32_t incl = wave_incl_scan(sum);  // counts in this lane's bins and every bin above
+        const uint64_t hit = wave_ballot(incl >= need);
+        if (hit == 0) continue;
+        if (lane == static_cast<uint32_t>(__builtin_ctzll(hit))) {
+            uint32_t acc = incl - sum;  // < need: the lanes above fall short
+            uint32_t found = 0;
+            bool done = false;
+#pragma unroll
+            for (int i = 7; i >= 0; i--) {
+                acc += c[i];
+                if (!done && acc >= need) {
+                    found = static_cast<uint32_t>(i);
+                    done = true;
+                }
             }
+            const uint32_t bin = lo + found;
+            if (bin > 0) atomicMax(&misc[M_THR + g], h.base[g] + (bin << h.shift[g]));
         }
     }
-    uint32_t total;
-    uint32_t pos = block_excl_scan<kBlock>(mine, lds_tmp(), &total);  // its barriers separate the reads above
-#pragma unroll
-    for (uint32_t k = 0; k < kBufCap / kBlock; k++)
-        if (keepmask & (1u << k)) buf[pos++] = e[k];
-    __syncthreads();
-    return total;
 }
 
-// Exact prune: raises each tracked threshold to its order statistic over the
-// buffer, then compacts; returns the new fill.
-__device__ __forceinline__ uint32_t prune_buffer(Targets tg, uint32_t bufn) {
-    __syncthreads();  // the caller's buffer writes
-    const Sel3 s = buf_select(bufn, 0, false, tg);
-    uint32_t* misc = lds_misc();
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int g = 0; g < 3; g++)
-            if (tg.need[g] && s.T[g] != ~0ull)
-                misc[M_THR + g] = __float_as_uint(fmaxf(__uint_as_float(misc[M_THR + g]), comp_threshold(s.T[g])));
-    }
-    __syncthreads();
-    return compact_buffer(tg, bufn);
-}
-
-// Lower bounds for the thresholds from one tile: k[g] is this thread's
+// Lower bounds for the thresholds from the first tile: k[g] is this thread's
 // largest key among its 8 ids relevant to target g (0: none).  For each
 // target the group maxima are histogrammed on the 11 bits below the prefix
 // they all share; the digit of the need-th largest gives a value with at
-// least `need` of the tile's elements at or above it.
-__device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2) {
+// least `need` of the tile's elements at or above it, which raises
+// misc[M_THR + g].  top[g] gets the largest canon key among the tile's
+// elements relevant to target g (0: none).  Block-wide, ends with a barrier.
+__device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t top[3]) {
     const uint32_t tid = threadIdx.x;
     uint32_t* h3 = lds_hist3();
     uint32_t* misc = lds_misc();
@@ -423,18 +438,19 @@ __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1
         mx[g] = (tg.need[g] && k[g]) ? static_cast<unsigned long long>(~k[g]) : 0ull;
     }
     block_minmax3(mn, mx);
-    int lo[3], top[3];
+    int lo[3], tb[3];
 #pragma unroll
     for (int g = 0; g < 3; g++) {
-        top[g] = mn[g] <= mx[g] ? high_bit64(mn[g] ^ mx[g]) + 1 : 0;
-        lo[g] = top[g] > 11 ? top[g] - 11 : 0;
+        tb[g] = mn[g] <= mx[g] ? high_bit64(mn[g] ^ mx[g]) + 1 : 0;
+        lo[g] = tb[g] > 11 ? tb[g] - 11 : 0;
+        top[g] = mn[g] <= mx[g] ? canon_key(key_to_float(~static_cast<uint32_t>(mn[g]))) : 0u;
     }
     for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < 3; g++)
         if (tg.need[g] && k[g] != 0u)
-            atomicAdd(&h3[g * kBins + (((~k[g]) >> lo[g]) & ((1u << (top[g] - lo[g])) - 1u))], 1u);
+            atomicAdd(&h3[g * kBins + (((~k[g]) >> lo[g]) & ((1u << (tb[g] - lo[g])) - 1u))], 1u);
     __syncthreads();
     hist_find3(tg.need);
     if (tid == 0) {
@@ -443,11 +459,11 @@ __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1
             const uint32_t d = misc[M_SEL + 2 * g];
             if (tg.need[g] && d != 0xFFFFFFFFu) {
                 // the bin's largest ~key (its lowest key): shared prefix, digit, ones below
-                const uint32_t pre = top[g] >= 32 ? 0u : (static_cast<uint32_t>(mn[g]) >> top[g]) << top[g];
+                const uint32_t pre = tb[g] >= 32 ? 0u : (static_cast<uint32_t>(mn[g]) >> tb[g]) << tb[g];
                 const uint32_t nk = pre | (d << lo[g]) | ((1u << lo[g]) - 1u);
                 const uint32_t key = ~nk;
                 const float b = key <= 0x007FFFFFu ? -INFINITY : key_to_float(key);
-                misc[M_THR + g] = __float_as_uint(fmaxf(__uint_as_float(misc[M_THR + g]), b));
+                misc[M_THR + g] = max(misc[M_THR + g], canon_key(b));
             }
         }
     }
@@ -476,14 +492,93 @@ __device__ __forceinline__ void load_tile(const float* rowp, const uint32_t* mro
 }
 
 // Emission mask of this thread's tile elements under the thresholds.
-__device__ __forceinline__ uint32_t emit_mask(const Targets& tg, const float thr[3], const float (&v)[kVec][4],
+__device__ __forceinline__ uint32_t emit_mask(float tA, float tR, float tL, const float (&v)[kVec][4],
                                               uint32_t valid_bits, uint32_t pen_bits, uint32_t al_bits) {
     uint32_t emit = 0;
 #pragma unroll
-    for (int e = 0; e < kVec * 4; e++)
-        if (((valid_bits >> e) & 1u) && keep_entry(tg, thr, v[e >> 2][e & 3], (pen_bits >> e) & 1u, (al_bits >> e) & 1u))
-            emit |= 1u << e;
-    return emit;
+    for (int e = 0; e < kVec * 4; e++) {
+        const bool k = keep3(v[e >> 2][e & 3], (pen_bits >> e) & 1u, (al_bits >> e) & 1u, tA, tR, tL);
+        emit |= static_cast<uint32_t>(k) << e;
+    }
+    return emit & valid_bits;
+}
+
+// Buffer entry of element e of this thread's tile.
+__device__ __forceinline__ uint2 make_entry(float y, uint32_t id, uint32_t pen_bits, uint32_t al_bits, int e) {
+    return make_uint2(__float_as_uint(y), id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
+                                              (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
+}
+
+// Per-tile work of every thread before the candidates: logsumexp partials of
+// the raw logits, the penalties (v becomes the penalized y) and the flags.
+// lsum is sum exp(x - lref) over this thread's ids; ids past the row hold
+// -inf and add 0; a tile whose terms grow past 2^100 moves lref to its own
+// maximum.
+struct TileFlags {
+    uint32_t valid, pen, al;
+};
+
+__device__ __forceinline__ TileFlags tile_prep(float (&v)[kVec][4], const uint32_t (&mw)[kVec], uint32_t tb,
+                                               uint32_t n, const RowMode& m, const tsm_row_params& P,
+                                               bool fast_hist, bool track_pen, float& lref, double& lsum,
+                                               uint32_t& nallow) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t tl = min(kTile, n - tb);
+    TileFlags fl;
+    fl.valid = (1u << (kVec * 4)) - 1u;
+    if (tl < kTile) {  // the row's last, partial tile
+        fl.valid = 0;
+#pragma unroll
+        for (int e = 0; e < kVec * 4; e++)
+            if (4u * ((e >> 2) * kBlock + tid) + (e & 3) < tl) fl.valid |= 1u << e;
+    }
+    if (m.logprobs) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < kVec * 4; e++)
+            sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
+        if (!(sum < 0x1p100f)) {
+            float tmax = lref;
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++) tmax = fmaxf(tmax, v[e >> 2][e & 3]);
+            lsum *= exp2(static_cast<double>(lref - tmax) * 1.4426950408889634);
+            lref = tmax;
+            sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++)
+                sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
+        }
+        lsum += static_cast<double>(sum);
+    }
+    fl.pen = 0;
+    fl.al = 0;
+    uint32_t* misc = lds_misc();
+    uint2* pen = lds_pen();
+#pragma unroll
+    for (int j = 0; j < kVec; j++) {
+        const uint32_t id0 = tb + 4u * (j * kBlock + tid);
+        if (m.penal && fast_hist && id0 < n) {
+            const uint32_t bits4 = (lds_bitmap()[id0 >> 5] >> (id0 & 31u)) & 0xFu;  // 4 ids of one word
+            if (bits4) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (((bits4 >> q) & 1u) && id0 + q < n) {
+                        const float x = v[j][q];
+                        v[j][q] = penalize(x, history_count(id0 + q), m, P);
+                        fl.pen |= 1u << (j * 4 + q);
+                        if (track_pen) {
+                            const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
+                            if (pos < kPenCap) pen[pos] = make_uint2(__float_as_uint(x), id0 + q);
+                        }
+                    }
+                }
+            }
+        }
+        if (m.constrained) fl.al |= ((mw[j] >> (id0 & 31u)) & 0xFu) << (j * 4);
+    }
+    fl.al &= fl.valid;
+    nallow += __popc(fl.al);
+    return fl;
 }
 
 // After the streaming pass: logsumexp and allowed count, then the pick (or
@@ -745,20 +840,31 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     if (!fast_hist) tg0.need[SK_RAW] = 0u;
     const bool track_pen = tg.need[SK_RAW] > 0 && m.penal;
 
+    const bool tracking = (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
     if (tid == 0) {
         misc[M_BUFN] = 0;
         misc[M_PENN] = 0;
+        misc[M_OVF] = 0;
         misc[M_FLAGS] = fast_hist ? 0u : ROWF_SLOW_HISTORY;
-        for (int g = 0; g < 3; g++) misc[M_THR + g] = __float_as_uint(-INFINITY);
+        for (int g = 0; g < 3; g++) misc[M_THR + g] = tg.need[g] ? kKeyNegInf : kKeyUntracked;
     }
+    if (tracking)  // first used after the first tile's barriers
+        for (uint32_t i = tid; i < 3 * kSBins; i += kBlock) lds_shist()[i] = 0;
     // tiles t+1 and t+2 are in flight while tile t is processed
     float v[kVec][4], vn[kVec][4], vn2[kVec][4];
     uint32_t mw[kVec], mwn[kVec], mwn2[kVec];
     load_tile<kVecLoads>(rowp, mrow, 0, n, v, mw);             // in flight while the lookup is built
     if (kTile < n) load_tile<kVecLoads>(rowp, mrow, kTile, n, vn, mwn);
     if (m.penal && fast_hist) history_build(f.hist, hlen, n);  // barriers inside
-    float thr[3] = {-INFINITY, -INFINITY, -INFINITY};
-    const bool tracking = (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
+
+    SHist sh;
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        sh.base[g] = kKeyUntracked;
+        sh.shift[g] = 0;
+    }
+    bool wave_track = tracking;  // uniform per wave; cleared once the buffer overflows
+    const uint32_t wid = tid / kWave, lane = lane_id();
 
     // ---------------- streaming pass ----------------
     double lsum = 0.0;  // sum of exp(x - lref) over this thread's ids
@@ -770,146 +876,117 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         lref = t0 == -INFINITY ? 0.0f : t0;
     }
     uint32_t nallow = 0;
-    uint32_t bufn = 0;  // candidate buffer fill (uniform)
     const uint32_t ntiles = (n + kTile - 1) / kTile;
-    for (uint32_t t = 0; t < ntiles; t++) {
-        const uint32_t tb = t * kTile;
-        const uint32_t tl = min(kTile, n - tb);
-        if (t + 2 < ntiles) load_tile<kVecLoads>(rowp, mrow, tb + 2 * kTile, n, vn2, mwn2);  // prefetch
-        uint32_t valid_bits = (1u << (kVec * 4)) - 1u;
-        if (tl < kTile) {  // the row's last, partial tile
-            valid_bits = 0;
+    if (2 < ntiles) load_tile<kVecLoads>(rowp, mrow, 2 * kTile, n, vn2, mwn2);  // prefetch
+    {
+        // first tile: block-wide, so the thresholds can start from the tile's
+        // own group-max bounds
+        const TileFlags fl = tile_prep(v, mw, 0, n, m, P, fast_hist, track_pen, lref, lsum, nallow);
+        if (tracking) {
+            float th[3];
 #pragma unroll
-            for (int e = 0; e < kVec * 4; e++)
-                if (4u * ((e >> 2) * kBlock + tid) + (e & 3) < tl) valid_bits |= 1u << e;
-        }
-        // logsumexp partials: sum of exp(x - ref) with a per-thread reference
-        // (ids past the row hold -inf and add 0); a tile whose terms grow past
-        // 2^100 moves the reference to its own maximum
-        if (m.logprobs) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int e = 0; e < kVec * 4; e++)
-                sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
-            if (!(sum < 0x1p100f)) {
-                float tmax = lref;
-#pragma unroll
-                for (int e = 0; e < kVec * 4; e++) tmax = fmaxf(tmax, v[e >> 2][e & 3]);
-                lsum *= exp2(static_cast<double>(lref - tmax) * 1.4426950408889634);
-                lref = tmax;
-                sum = 0.0f;
-#pragma unroll
-                for (int e = 0; e < kVec * 4; e++)
-                    sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
+            for (int g = 0; g < 3; g++) th[g] = thr_float(tg.need[g] ? kKeyNegInf : kKeyUntracked);
+            uint32_t emit = 0, total = 0, pos0 = 0;
+            bool bound = ntiles > 1;
+            if (!bound) {
+                emit = emit_mask(th[0], th[1], th[2], v, fl.valid, fl.pen, fl.al);
+                pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+                bound = total > kBufCap;
             }
-            lsum += static_cast<double>(sum);
+            if (bound) {
+                uint32_t k[3] = {0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < kVec * 4; e++) {
+                    if (!((fl.valid >> e) & 1u)) continue;
+                    const float y = v[e >> 2][e & 3];
+                    k[SK_ALL] = max(k[SK_ALL], canon_key(y));
+                    if (!((fl.pen >> e) & 1u)) k[SK_RAW] = max(k[SK_RAW], canon_key(y));
+                    if ((fl.al >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
+                }
+                uint32_t top[3];
+                tile_bounds(tg, k[0], k[1], k[2], top);
+#pragma unroll
+                for (int g = 0; g < 3; g++) {
+                    const uint32_t b = misc[M_THR + g];
+                    th[g] = thr_float(b);
+                    sh.base[g] = b;
+                    const uint32_t span = top[g] > b ? top[g] - b : 0u;
+                    const int bits = 32 - __clz(span);
+                    sh.shift[g] = bits > 8 ? static_cast<uint32_t>(bits - 8) : 0u;
+                }
+                emit = emit_mask(th[0], th[1], th[2], v, fl.valid, fl.pen, fl.al);
+                pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+            }
+            if (total > kBufCap) {  // uniform: stop tracking, the finish re-reads
+                if (tid == 0) misc[M_OVF] = 1u;
+                wave_track = false;
+                emit = 0;
+                total = 0;
+            }
+            uint32_t pos = pos0;
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++)
+                if ((emit >> e) & 1u) {
+                    const float y = v[e >> 2][e & 3];
+                    buf[pos++] = make_entry(y, 4u * ((e >> 2) * kBlock + tid) + (e & 3), fl.pen, fl.al, e);
+                    if (bound) count_kept(y, (fl.pen >> e) & 1u, (fl.al >> e) & 1u, th[0], th[1], th[2], sh);
+                }
+            if (tid == 0) misc[M_BUFN] = total;
+            __syncthreads();
         }
-        // penalties (v becomes the penalized y) and flags
-        uint32_t pen_bits = 0, al_bits = 0;
 #pragma unroll
         for (int j = 0; j < kVec; j++) {
-            const uint32_t id0 = tb + 4u * (j * kBlock + tid);
-            if (m.penal && fast_hist && id0 < n) {
-                const uint32_t bits4 = (lds_bitmap()[id0 >> 5] >> (id0 & 31u)) & 0xFu;  // 4 ids of one word
-                if (bits4) {
+            mw[j] = mwn[j];
+            mwn[j] = mwn2[j];
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        if (((bits4 >> q) & 1u) && id0 + q < n) {
-                            const float x = v[j][q];
-                            v[j][q] = penalize(x, history_count(id0 + q), m, P);
-                            pen_bits |= 1u << (j * 4 + q);
-                            if (track_pen) {
-                                const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
-                                if (pos < kPenCap) pen[pos] = make_uint2(__float_as_uint(x), id0 + q);
-                            }
-                        }
-                    }
-                }
+            for (int q = 0; q < 4; q++) {
+                v[j][q] = vn[j][q];
+                vn[j][q] = vn2[j][q];
             }
-            if (m.constrained) al_bits |= ((mw[j] >> (id0 & 31u)) & 0xFu) << (j * 4);
         }
-        al_bits &= valid_bits;
-        nallow += __popc(al_bits);
-        // candidates at or above the thresholds
-        if (tracking) {
-            uint32_t emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
-            if (t == 0) {
-                // first tile: block-wide, so the thresholds can start from the
-                // tile's own group-max bounds
-                uint32_t total;
-                uint32_t pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
-                if (total > kBufCap) {
-                    uint32_t k[3] = {0u, 0u, 0u};
+    }
+    for (uint32_t t = 1; t < ntiles; t++) {
+        const uint32_t tb = t * kTile;
+        if (t + 2 < ntiles) load_tile<kVecLoads>(rowp, mrow, tb + 2 * kTile, n, vn2, mwn2);  // prefetch
+        const TileFlags fl = tile_prep(v, mw, tb, n, m, P, fast_hist, track_pen, lref, lsum, nallow);
+        // candidates at or above the thresholds as they are now (they only
+        // rise, so any value read is valid); no barriers: each wave reserves
+        // its slots with one LDS atomic
+        if (wave_track && wave_uniform(lds_load_relaxed(&misc[M_OVF])) != 0u)
+            wave_track = false;  // the buffer overflowed: the finish re-reads the row
+        if (wave_track) {
+            const float tA = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)])));
+            const float tR = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)])));
+            const float tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
+            const float tmin = fminf(tA, fminf(tR, tL));
+            float mx = v[0][0];
 #pragma unroll
-                    for (int e = 0; e < kVec * 4; e++) {
-                        if (!((valid_bits >> e) & 1u)) continue;
-                        const float y = v[e >> 2][e & 3];
-                        k[SK_ALL] = max(k[SK_ALL], canon_key(y));
-                        if (!((pen_bits >> e) & 1u)) k[SK_RAW] = max(k[SK_RAW], canon_key(y));
-                        if ((al_bits >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
-                    }
-                    tile_bounds(tg, k[0], k[1], k[2]);
-                    load_thr(thr);
-                    emit = emit_mask(tg, thr, v, valid_bits, pen_bits, al_bits);
-                    pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
-                }
-                if (total > kBufCap) {  // uniform: stop tracking, the finish re-reads
-                    if (tid == 0) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
-                    tg.need[SK_ALL] = tg.need[SK_RAW] = tg.need[SK_ALLOWED] = 0;
-                    emit = 0;
-                    total = 0;
-                }
-                uint32_t pos = pos0;
-#pragma unroll
-                for (int e = 0; e < kVec * 4; e++)
-                    if ((emit >> e) & 1u) {
-                        const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
-                        buf[pos++] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
-                                                id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
-                                                    (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
-                    }
-                if (tid == 0) misc[M_BUFN] = total;
-                __syncthreads();
-            } else {
-                // later tiles: each wave reserves its slots with one LDS atomic,
-                // no barrier; a reservation past the buffer flags the row
+            for (int e = 1; e < kVec * 4; e++) mx = fmaxf(mx, v[e >> 2][e & 3]);
+            if (wave_ballot(mx >= tmin) != 0) {
+                const uint32_t emit = emit_mask(tA, tR, tL, v, fl.valid, fl.pen, fl.al);
                 const uint32_t cnt = __popc(emit);
                 const uint32_t incl = wave_incl_scan(cnt);
                 const uint32_t wtot = wave_read(incl, kWave - 1);
                 if (wtot) {
                     uint32_t base = 0;
-                    if (lane_id() == kWave - 1) base = atomicAdd(&misc[M_BUFN], wtot);
+                    if (lane == kWave - 1) base = atomicAdd(&misc[M_BUFN], wtot);
                     base = wave_read(base, kWave - 1);
                     if (base + wtot <= kBufCap) {
                         uint32_t pos = base + incl - cnt;
 #pragma unroll
                         for (int e = 0; e < kVec * 4; e++)
                             if ((emit >> e) & 1u) {
+                                const float y = v[e >> 2][e & 3];
                                 const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
-                                buf[pos++] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
-                                                        id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
-                                                            (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
+                                buf[pos++] = make_entry(y, id, fl.pen, fl.al, e);
+                                count_kept(y, (fl.pen >> e) & 1u, (fl.al >> e) & 1u, tA, tR, tL, sh);
                             }
-                    } else if (lane_id() == 0) {
-                        atomicOr(&misc[M_FLAGS], static_cast<uint32_t>(ROWF_BUF_OVERFLOW));
+                    } else if (lane == 0) {
+                        atomicOr(&misc[M_OVF], 1u);
                     }
                 }
             }
-            // every second tile: a sync point that prunes a filling buffer
-            if ((t & 1u) == 1u && t + 1 < ntiles) {
-                __syncthreads();
-                const uint32_t fl = misc[M_FLAGS];
-                bufn = misc[M_BUFN];
-                __syncthreads();  // every wave has read the fill before anyone adds to it
-                if (fl & ROWF_BUF_OVERFLOW) {
-                    tg.need[SK_ALL] = tg.need[SK_RAW] = tg.need[SK_ALLOWED] = 0;  // uniform
-                } else if (bufn > kPruneAt) {
-                    bufn = prune_buffer(tg, bufn);
-                    if (tid == 0) misc[M_BUFN] = bufn;
-                    load_thr(thr);
-                    __syncthreads();
-                }
-            }
+            if (wid == (t & (kBlock / kWave - 1))) raise_thresholds(tg, sh);
         }
 #pragma unroll
         for (int j = 0; j < kVec; j++) {
@@ -923,7 +1000,12 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         }
     }
     __syncthreads();
-    bufn = tracking ? min(misc[M_BUFN], kBufCap) : 0u;
+    uint32_t bufn = 0;
+    if (tracking) {
+        const uint32_t fill = misc[M_BUFN];
+        if (tid == 0 && (fill > kBufCap || misc[M_OVF] != 0u)) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
+        bufn = min(fill, kBufCap);
+    }
     finish_row(a, f, tg0, nlp, lref, lsum, nallow, bufn);
 }
 

@@ -42,7 +42,9 @@ constexpr uint32_t kOffPen = kOffBuf + kBufCap * 8;              // uint2[kPenCa
 constexpr uint32_t kOffMisc = kOffPen + kPenCap * 8;             // u32[64]
 constexpr uint32_t kOffMiscD = kOffMisc + 64 * 4;                // f64[32]
 constexpr uint32_t kOffTmp = kOffMiscD + 32 * 8;                 // u32[64] scan scratch
-constexpr uint32_t kSmem = kOffTmp + 64 * 4;
+constexpr uint32_t kSBins = 512;                                 // stream histogram bins per threshold
+constexpr uint32_t kOffSHist = kOffTmp + 64 * 4;                 // 3 x u32[kSBins]
+constexpr uint32_t kSmem = kOffSHist + 3 * kSBins * 4;
 static_assert(kOffGather % 8 == 0 && (kOffHist + kBins * 4) % 8 == 0 && kOffBuf % 8 == 0 && kOffPen % 8 == 0 &&
                   kOffMiscD % 8 == 0,
               "u64 / f64 LDS records are 8-byte aligned");
@@ -61,7 +63,8 @@ enum : uint32_t {  // misc word indices
     M_BUFN = 11,    // candidate buffer fill
     M_PENN = 12,    // penalized list fill (may exceed kPenCap: overflow)
     M_FLAGS = 13,   // ROWF_* bits
-    M_THR = 16,     // 3 thresholds (float bits): all, raw, allowed
+    M_THR = 16,     // 3 stream thresholds (canon keys): all, raw, allowed
+    M_OVF = 19,     // nonzero once a reservation ran past the candidate buffer
     M_SEL = 20,     // 3 x 2 hist_find3 results
     M_RED = 32,     // 32 words of reduction results
 };

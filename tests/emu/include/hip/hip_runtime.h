@@ -138,6 +138,37 @@ inline int emu_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool
     return got;
 }
 
+// Ballot over the 64 lanes of the wave (every lane must take part).
+inline unsigned long long __ballot(int pred) {
+    uint64_t* slots = ::emu::wave_slots();
+    const int lane = ::emu::lane_id();
+    const int bank = ::emu::next_bank();
+    slots[bank * 64 + lane] = pred != 0;
+    ::emu::wave_sync();
+    unsigned long long m = 0;
+    for (int i = 0; i < 64; i++)
+        if (slots[bank * 64 + i]) m |= 1ull << i;
+    return m;
+}
+// Used by the kernels only where the whole wave is active: lane 0 is the first.
+#define __builtin_amdgcn_readfirstlane(v) emu_shfl((v), 0)
+inline uint32_t __builtin_amdgcn_mbcnt_lo(uint32_t mask, uint32_t acc) {
+    const int lane = ::emu::lane_id();
+    const uint32_t below = lane >= 32 ? 0xFFFFFFFFu : ((1u << lane) - 1u);
+    return acc + static_cast<uint32_t>(__builtin_popcount(mask & below));
+}
+inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t mask, uint32_t acc) {
+    const int lane = ::emu::lane_id();
+    const uint32_t below = lane < 32 ? 0u : ((1ull << (lane - 32)) - 1ull);
+    return acc + static_cast<uint32_t>(__builtin_popcount(mask & below));
+}
+#define __HIP_MEMORY_SCOPE_WORKGROUP 3
+template <class T>
+inline T __hip_atomic_load(T* p, int order, int) {
+    return std::atomic_ref<T>(*p).load(order == __ATOMIC_RELAXED ? std::memory_order_relaxed
+                                                                 : std::memory_order_seq_cst);
+}
+
 template <class T>
 inline T __shfl_xor(T v, int mask, int width = 64) {
     const int lane = ::emu::lane_id();
