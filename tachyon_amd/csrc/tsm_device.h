@@ -197,6 +197,34 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 __device__ __forceinline__ uint32_t lds_load_relaxed(uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+// Publishing a count of records written to LDS: every lane fences its LDS
+// writes and then raises the count (read-modify-write, so the updates of all
+// lanes form one release sequence); a reader loads the count and fences
+// before reading the records.  The fences order LDS operations only
+// ("local"), so neither side waits for the wave's global loads in flight, as
+// a plain release / acquire at workgroup scope would (it orders global
+// memory too).
+__device__ __forceinline__ void lds_publish_max(uint32_t* p, uint32_t v) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint32_t lds_load_acquire(uint32_t* p) {
+    const uint32_t v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    return v;
+}
+
+// Workgroup barrier for LDS communication.  Every exchange between the
+// threads of a workgroup in these kernels goes through LDS (global memory is
+// only read, or written for the host), so the barrier fences LDS alone: a
+// __syncthreads() would also wait for every global load in flight, which
+// stalls the row's prefetched tiles at each barrier.
+#define TSM_LDS_SYNC()                                                   \
+    do {                                                                 \
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  \
+        __builtin_amdgcn_s_barrier();                                    \
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");  \
+    } while (0)
 
 // Exclusive prefix sum over the block; `tmp` holds >= nwaves+1 words of LDS.
 // Returns the prefix; *total gets the block sum.  Contains two barriers.
@@ -206,7 +234,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* tmp, u
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
     uint32_t inc = wave_incl_scan(v);
     if (lane == kWave - 1) tmp[wid] = inc;
-    __syncthreads();
+    TSM_LDS_SYNC();
     uint32_t before = 0, all = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
@@ -214,7 +242,7 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* tmp, u
         before += (w < wid) ? t : 0u;
         all += t;
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     *total = all;
     return before + inc - v;
 }
@@ -224,11 +252,11 @@ __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* tmp) {
     constexpr int NW = NT / kWave;
     v = wave_sum(v);
     if ((threadIdx.x & (kWave - 1)) == 0) tmp[threadIdx.x / kWave] = v;
-    __syncthreads();
+    TSM_LDS_SYNC();
     uint32_t all = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) all += tmp[w];
-    __syncthreads();
+    TSM_LDS_SYNC();
     return all;
 }
 
@@ -237,11 +265,11 @@ __device__ __forceinline__ uint32_t block_min(uint32_t v, uint32_t* tmp) {
     constexpr int NW = NT / kWave;
     v = wave_min(v);
     if ((threadIdx.x & (kWave - 1)) == 0) tmp[threadIdx.x / kWave] = v;
-    __syncthreads();
+    TSM_LDS_SYNC();
     uint32_t all = 0xFFFFFFFFu;
 #pragma unroll
     for (int w = 0; w < NW; w++) all = tmp[w] < all ? tmp[w] : all;
-    __syncthreads();
+    TSM_LDS_SYNC();
     return all;
 }
 
@@ -275,7 +303,7 @@ __device__ __forceinline__ void hist_find(const uint32_t* hist, uint32_t need, u
             run += c[i];
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 }  // namespace tsm

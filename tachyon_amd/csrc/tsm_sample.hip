@@ -44,6 +44,7 @@ enum : uint32_t {
 };
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;     // canon_key(-inf): a threshold every non-NaN value passes
 constexpr uint32_t kKeyUntracked = 0xFFFFFFFFu;  // threshold of a target not tracked: reads as NaN, keeps nothing
+constexpr uint32_t kBigEmit = 64;                // a wave's candidates in one tile past which it tightens first
 constexpr uint32_t kEntPen = 0x80000000u;    // buffer entry flags (ids < 2^22)
 constexpr uint32_t kEntAllowed = 0x40000000u;
 constexpr uint32_t kEntId = 0x003FFFFFu;
@@ -76,6 +77,10 @@ __device__ __forceinline__ uint32_t* lds_bitmap() { return reinterpret_cast<uint
 __device__ __forceinline__ uint32_t* lds_hkey() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashKey); }
 __device__ __forceinline__ uint32_t* lds_hcnt() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashCnt); }
 __device__ __forceinline__ uint32_t* lds_shist() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSHist); }
+__device__ __forceinline__ uint32_t* lds_seg_pub() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg); }
+__device__ __forceinline__ uint32_t* lds_seg_done() {
+    return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg + (kBlock / kWave) * 4);
+}
 
 // The running thresholds are canon keys in LDS (misc[M_THR + g]), raised
 // only by atomicMax.  As a float, y >= key_to_float(k) holds exactly when
@@ -94,14 +99,14 @@ __device__ void history_build(const uint32_t* hist, uint32_t hlen, uint32_t n) {
     uint32_t* bm = lds_bitmap();
     uint32_t* hk = lds_hkey();
     uint32_t* hc = lds_hcnt();
-    __syncthreads();
+    TSM_LDS_SYNC();
     const uint32_t words = (n + 31) / 32;
     for (uint32_t i = tid; i < words; i += kBlock) bm[i] = 0;
     for (uint32_t i = tid; i < kHashSlots; i += kBlock) {
         hk[i] = 0;
         hc[i] = 0;
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     for (uint32_t h = tid; h < hlen; h += kBlock) {
         const uint32_t id = hist[h];
         if (id >= n) continue;  // ids past the vocabulary cap are ignored (sampler.rs:171)
@@ -116,7 +121,7 @@ __device__ void history_build(const uint32_t* hist, uint32_t hlen, uint32_t n) {
             s = (s + 1) & (kHashSlots - 1);
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 // Count of `id` in the history (its bitmap bit is set).
@@ -154,7 +159,7 @@ __device__ __forceinline__ void block_excl_scan3(const uint32_t v[3], uint32_t b
         inc[g] = wave_incl_scan(v[g]);
         if (lane == kWave - 1) tmp[g * NW + wid] = inc[g];
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 #pragma unroll
     for (int g = 0; g < 3; g++) {
         uint32_t b = 0, all = 0;
@@ -166,7 +171,7 @@ __device__ __forceinline__ void block_excl_scan3(const uint32_t v[3], uint32_t b
         before[g] = b + inc[g] - v[g];
         total[g] = all;
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 // For up to three histograms (kBins bins each, ascending digit = best
@@ -197,7 +202,7 @@ __device__ void hist_find3(const uint32_t need[3]) {
             res[2 * g + 1] = first ? before[g] : before[g] + c0[g];
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 // Block-wide min and max of up to three u64 values per thread (one barrier
@@ -219,7 +224,7 @@ __device__ __forceinline__ void block_minmax3(unsigned long long mn[3], unsigned
             t[(2 * g + 1) * NW + wid] = mx[g];
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 #pragma unroll
     for (int g = 0; g < 3; g++) {
         unsigned long long a = ~0ull, b = 0;
@@ -231,7 +236,7 @@ __device__ __forceinline__ void block_minmax3(unsigned long long mn[3], unsigned
         mn[g] = a;
         mx[g] = b;
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 __device__ __forceinline__ int high_bit64(unsigned long long v) { return v ? 63 - __builtin_clzll(v) : -1; }
@@ -297,7 +302,7 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
 #pragma unroll
         for (int g = 0; g < 3; g++) lo[g] = top[g] > 11 ? top[g] - 11 : 0;
         for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
-        __syncthreads();
+        TSM_LDS_SYNC();
         for (uint32_t i = tid; i < bufn; i += kBlock) {
             const uint2 e = buf[i];
 #pragma unroll
@@ -318,7 +323,7 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
                 atomicAdd(&h3[SK_RAW * kBins + static_cast<uint32_t>((c >> l1) & ((1ull << (t1 - l1)) - 1ull))], 1u);
             }
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
         uint32_t nd[3];
 #pragma unroll
         for (int g = 0; g < 3; g++) nd[g] = active[g] ? need[g] : 0u;
@@ -330,7 +335,7 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
             before[g] = misc[M_SEL + 2 * g + 1];
             inbin[g] = (active[g] && d[g] != 0xFFFFFFFFu) ? h3[g * kBins + d[g]] : 0u;
         }
-        __syncthreads();  // before the next round clears the histograms / rewrites M_SEL
+        TSM_LDS_SYNC();  // before the next round clears the histograms / rewrites M_SEL
 #pragma unroll
         for (int g = 0; g < 3; g++) {
             if (!active[g]) continue;
@@ -351,54 +356,56 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
     return out;
 }
 
-// Whether a (penalized) value y is kept by one of the three thresholds: the
-// raw one applies to non-penalized ids, the allowed one to allowed ids.
-// Branch-free; an untracked threshold is NaN and keeps nothing.
-__device__ __forceinline__ bool keep3(float y, bool pen, bool al, float tA, float tR, float tL) {
-    return static_cast<bool>((y >= tA) | (!pen & (y >= tR)) | (al & (y >= tL)));
+// Stream emission rule: an element that is not penalized is kept when it is
+// at or above the all / raw threshold (tAR, the lower of the two), or when it
+// is allowed and at or above the allowed threshold.  Branch-free; an
+// untracked threshold is NaN and keeps nothing.  Penalized ids never go to
+// the buffer during the stream: they are listed with their raw values and
+// join the buffer at the end if their penalized value passes.
+__device__ __forceinline__ bool keep2(float y, bool al, float tAR, float tL) {
+    return static_cast<bool>((y >= tAR) | (al & (y >= tL)));
 }
 
-// Geometry of the stream histograms: bin = (key - base) >> shift, clamped to
-// the last bin; base is a threshold's key after the first tile (every key a
-// threshold keeps afterwards is at or above it) and the shift puts the first
-// tile's largest key near the middle of the bins.
+// Two stream histograms of the keys of emitted (non-penalized) elements:
+// H[0] counts every one (it raises the all and raw thresholds), H[1] the
+// allowed ones (the allowed threshold).  bin = (key - base) >> shift, clamped
+// to the last bin; keys below base are not counted.  A bin's count is a
+// number of distinct elements of the row whose keys are at or above the bin's
+// lower edge, which is all a raise needs.
 struct SHist {
-    uint32_t base[3], shift[3];
+    uint32_t base[2], shift[2];
 };
 
-// Counts a kept element in the histogram of each threshold that keeps it.
-__device__ __forceinline__ void count_kept(float y, bool pen, bool al, float tA, float tR, float tL, const SHist& h) {
+__device__ __forceinline__ void count_kept(float y, bool al, const SHist& h) {
     uint32_t* sh = lds_shist();
     const uint32_t key = canon_key(y);
-    const bool c[3] = {y >= tA, static_cast<bool>(!pen & (y >= tR)), static_cast<bool>(al & (y >= tL))};
-#pragma unroll
-    for (int g = 0; g < 3; g++)
-        if (c[g] && key >= h.base[g]) atomicAdd(&sh[g * kSBins + min((key - h.base[g]) >> h.shift[g], kSBins - 1)], 1u);
+    if (key >= h.base[0]) atomicAdd(&sh[min((key - h.base[0]) >> h.shift[0], kSBins - 1)], 1u);
+    if (al && key >= h.base[1]) atomicAdd(&sh[kSBins + min((key - h.base[1]) >> h.shift[1], kSBins - 1)], 1u);
 }
 
-// One wave raises each tracked threshold to the lower edge of the highest
-// histogram bin at which the counts, summed from the top bin down, reach
-// need[g]: that many kept elements have keys at or above the edge, so no
-// element below it can be among the target's best.  Other waves keep adding
-// to the counts meanwhile; counts only grow, so whatever mix of old and new
-// counts is read is still a valid lower bound.  A bin that holds an element
-// has its edge at or below that element's key, so the edge never wraps.
-__device__ __forceinline__ void raise_thresholds(const Targets& tg, const SHist& h) {
+// One wave raises the tracked thresholds: for each, the lower edge of the
+// highest histogram bin at which the counts, summed from the top bin down,
+// reach need[g].  Other waves keep adding to the counts meanwhile; counts
+// only grow, so whatever mix of old and new counts is read is still a valid
+// lower bound.  A bin that holds an element has its edge at or below that
+// element's key, so the edge never wraps.
+__device__ __forceinline__ void raise_from(uint32_t hh, uint32_t need0, uint32_t g0, uint32_t need1, uint32_t g1,
+                                           const SHist& h) {
     const uint32_t lane = lane_id();
     uint32_t* misc = lds_misc();
+    const uint32_t lo = kSBins - 8u * (lane + 1u);  // lane 0 holds the 8 top bins
+    uint32_t* bins = lds_shist() + hh * kSBins + lo;
+    uint32_t c[8], sum = 0;
 #pragma unroll
-    for (int g = 0; g < 3; g++) {
-        const uint32_t need = tg.need[g];
+    for (int i = 0; i < 8; i++) {
+        c[i] = lds_load_relaxed(bins + i);
+        sum += c[i];
+    }
+    const uint32_t incl = wave_incl_scan(sum);  // counts in this lane's bins and every bin above
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const uint32_t need = k == 0 ? need0 : need1;
         if (!need) continue;
-        const uint32_t lo = kSBins - 8u * (lane + 1u);  // lane 0 holds the 8 top bins
-        uint32_t* bins = lds_shist() + g * kSBins + lo;
-        uint32_t c[8], sum = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            c[i] = lds_load_relaxed(bins + i);
-            sum += c[i];
-        }
-        const uint32_t incl = wave_incl_scan(sum);  // counts in this lane's bins and every bin above
         const uint64_t hit = wave_ballot(incl >= need);
         if (hit == 0) continue;
         if (lane == static_cast<uint32_t>(__builtin_ctzll(hit))) {
@@ -414,9 +421,57 @@ __device__ __forceinline__ void raise_thresholds(const Targets& tg, const SHist&
                 }
             }
             const uint32_t bin = lo + found;
-            if (bin > 0) atomicMax(&misc[M_THR + g], h.base[g] + (bin << h.shift[g]));
+            if (bin > 0) atomicMax(&misc[M_THR + (k == 0 ? g0 : g1)], h.base[hh] + (bin << h.shift[hh]));
         }
     }
+}
+
+// After the first tile each wave appends its candidates to a segment of its
+// own (segment w starts at seg0 + w * seg_cap) and publishes the segment's
+// fill.  The wave that raises the thresholds first counts what was published
+// since the last count: it claims each segment's new range with atomicMax on
+// the counted fill, so two raising waves never count an entry twice.
+__device__ __forceinline__ void count_published(const SHist& h, uint32_t seg0, uint32_t seg_cap) {
+    constexpr uint32_t NW = kBlock / kWave;
+    const uint32_t lane = lane_id();
+    uint32_t from = 0, to = 0;
+    if (lane < NW) {
+        to = lds_load_acquire(&lds_seg_pub()[lane]);
+        from = atomicMax(&lds_seg_done()[lane], to);
+        from = min(from, to);  // a raise that got further: nothing left here
+    }
+    const uint2* buf = lds_buf();
+    for (uint32_t w = 0; w < NW; w++) {
+        const uint32_t f = wave_read(from, w), e = wave_read(to, w);
+        const uint32_t base = seg0 + w * seg_cap;
+        // every reading lane acquires the fill itself (it is at least e:
+        // fills only grow), so each lane's reads are ordered after the writes
+        if (f < e) (void)lds_load_acquire(&lds_seg_pub()[w]);
+        for (uint32_t i = f + lane; i < e; i += kWave) {
+            const uint2 en = buf[base + i];
+            if (!(en.y & kEntPen)) count_kept(__uint_as_float(en.x), (en.y & kEntAllowed) != 0u, h);
+        }
+    }
+}
+
+__device__ __forceinline__ void raise_thresholds(const Targets& tg, const SHist& h) {
+    if (tg.need[SK_ALL] | tg.need[SK_RAW]) raise_from(0, tg.need[SK_ALL], SK_ALL, tg.need[SK_RAW], SK_RAW, h);
+    if (tg.need[SK_ALLOWED]) raise_from(1, tg.need[SK_ALLOWED], SK_ALLOWED, 0u, 0u, h);
+}
+
+// Wave-local lower bound for a threshold: with lm this lane's largest key
+// among its relevant elements (0: none), the need-th largest lane maximum
+// (need <= 64) has at least `need` elements of the row at or above it.
+// Bitwise search with one ballot per bit; returns 0 when fewer than `need`
+// lanes have a relevant element.
+__device__ __forceinline__ uint32_t wave_lane_bound(uint32_t lm, uint32_t need) {
+    uint32_t k = 0;
+#pragma nounroll
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t c = k | (1u << b);
+        if (static_cast<uint32_t>(__popcll(wave_ballot(lm >= c))) >= need) k = c;
+    }
+    return k;
 }
 
 // Lower bounds for the thresholds from the first tile: k[g] is this thread's
@@ -446,12 +501,12 @@ __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1
         top[g] = mn[g] <= mx[g] ? canon_key(key_to_float(~static_cast<uint32_t>(mn[g]))) : 0u;
     }
     for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
-    __syncthreads();
+    TSM_LDS_SYNC();
 #pragma unroll
     for (int g = 0; g < 3; g++)
         if (tg.need[g] && k[g] != 0u)
             atomicAdd(&h3[g * kBins + (((~k[g]) >> lo[g]) & ((1u << (tb[g] - lo[g])) - 1u))], 1u);
-    __syncthreads();
+    TSM_LDS_SYNC();
     hist_find3(tg.need);
     if (tid == 0) {
 #pragma unroll
@@ -467,40 +522,62 @@ __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1
             }
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
+// Loads one tile into registers.  With vector loads (row_stride a multiple of
+// 4, 16-byte aligned rows) every tile takes the same code path: ids past the
+// row are clamped to the row's last aligned float4, which lies inside the
+// row's allocation, and the consumer masks them (mask_tail).  A single path
+// matters: where two paths merge, the compiler copies the loaded registers,
+// and a copy waits for the load, which would stall the prefetch.  mp is the
+// row's mask, or any readable row of words when there is none (then unused).
 template <bool kVecLoads>
-__device__ __forceinline__ void load_tile(const float* rowp, const uint32_t* mrow, uint32_t tb, uint32_t n,
+__device__ __forceinline__ void load_tile(const float* rowp, const uint32_t* mp, uint32_t tb, uint32_t n,
                                           float (&v)[kVec][4], uint32_t (&mw)[kVec]) {
     const uint32_t tid = threadIdx.x;
+    if (kVecLoads) {
+        const uint32_t last = (n - 1u) & ~3u;
 #pragma unroll
-    for (int j = 0; j < kVec; j++) {
-        const uint32_t id = tb + 4u * (j * kBlock + tid);
-        if (kVecLoads && id + 3 < n) {
+        for (int j = 0; j < kVec; j++) {
+            const uint32_t id = min(tb + 4u * (j * kBlock + tid), last);
             const float4 f4 = *reinterpret_cast<const float4*>(rowp + id);
             v[j][0] = f4.x;
             v[j][1] = f4.y;
             v[j][2] = f4.z;
             v[j][3] = f4.w;
-        } else {
+            mw[j] = mp[id >> 5];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kVec; j++) {
+            const uint32_t id = tb + 4u * (j * kBlock + tid);
 #pragma unroll
             for (int q = 0; q < 4; q++) v[j][q] = (id + q < n) ? rowp[id + q] : -INFINITY;
+            mw[j] = mp[min(id, n - 1u) >> 5];
         }
-        mw[j] = (mrow && id < n) ? mrow[id >> 5] : 0u;
     }
 }
 
-// Emission mask of this thread's tile elements under the thresholds.
-__device__ __forceinline__ uint32_t emit_mask(float tA, float tR, float tL, const float (&v)[kVec][4],
-                                              uint32_t valid_bits, uint32_t pen_bits, uint32_t al_bits) {
+// The row's last tile: ids past the row read -inf (the clamped loads above
+// hold other ids' values there).
+__device__ __forceinline__ void mask_tail(float (&v)[kVec][4], uint32_t tb, uint32_t n) {
+    if (tb + kTile <= n) return;  // uniform
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < kVec * 4; e++)
+        if (tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3) >= n) v[e >> 2][e & 3] = -INFINITY;
+}
+
+// Emission mask of this thread's tile elements under the thresholds; elig
+// marks the elements that may be emitted (in the row, not penalized).
+__device__ __forceinline__ uint32_t emit_mask(float tAR, float tL, const float (&v)[kVec][4], uint32_t elig,
+                                              uint32_t al_bits) {
     uint32_t emit = 0;
 #pragma unroll
-    for (int e = 0; e < kVec * 4; e++) {
-        const bool k = keep3(v[e >> 2][e & 3], (pen_bits >> e) & 1u, (al_bits >> e) & 1u, tA, tR, tL);
-        emit |= static_cast<uint32_t>(k) << e;
-    }
-    return emit & valid_bits;
+    for (int e = 0; e < kVec * 4; e++)
+        emit |= static_cast<uint32_t>(keep2(v[e >> 2][e & 3], (al_bits >> e) & 1u, tAR, tL)) << e;
+    return emit & elig;
 }
 
 // Buffer entry of element e of this thread's tile.
@@ -510,75 +587,149 @@ __device__ __forceinline__ uint2 make_entry(float y, uint32_t id, uint32_t pen_b
 }
 
 // Per-tile work of every thread before the candidates: logsumexp partials of
-// the raw logits, the penalties (v becomes the penalized y) and the flags.
-// lsum is sum exp(x - lref) over this thread's ids; ids past the row hold
-// -inf and add 0; a tile whose terms grow past 2^100 moves lref to its own
-// maximum.
-struct TileFlags {
-    uint32_t valid, pen, al;
+// the raw logits and the flags.  Ids past the row hold -inf and add 0; a
+// tile whose terms grow past 2^100 moves the reference to its own maximum.  Penalized ids are not
+// candidates during the stream; with track_pen they are listed with their raw
+// values (the list holds every penalized id of the row: at most one entry per
+// distinct history id).
+constexpr float kL2E = 1.44269504088896341f;  // log2(e) in f32
+
+// Per-thread logsumexp accumulator: sum = sum of exp(x - ref) over this
+// thread's ids.  A term is exp2(fma(x, kL2E, nl)) with nl = -ref * kL2E
+// rounded; the rounding error eps = fma(ref, kL2E, nl) (exact) shifts every
+// exponent by the same amount, which corr = 2^-eps takes back out.
+struct LseAcc {
+    float ref = 0.0f, nl = 0.0f, corr = 1.0f;
+    double sum = 0.0;
+    __device__ __forceinline__ void set_ref(float r) {
+        ref = r;
+        nl = -r * kL2E;
+        corr = __builtin_amdgcn_exp2f(-__builtin_fmaf(r, kL2E, nl));
+    }
 };
 
-__device__ __forceinline__ TileFlags tile_prep(float (&v)[kVec][4], const uint32_t (&mw)[kVec], uint32_t tb,
-                                               uint32_t n, const RowMode& m, const tsm_row_params& P,
-                                               bool fast_hist, bool track_pen, float& lref, double& lsum,
-                                               uint32_t& nallow) {
+struct TileFlags {
+    uint32_t elig;  // in the row and not penalized
+    uint32_t valid; // in the row
+    uint32_t pen;   // penalized (in the row)
+    uint32_t al;    // allowed (in the row)
+};
+
+__device__ __forceinline__ TileFlags tile_prep(const float (&v)[kVec][4], const uint32_t (&mw)[kVec], uint32_t tb,
+                                               uint32_t n, bool logprobs, bool pen_lookup, bool track_pen,
+                                               bool constrained, LseAcc& L, uint32_t& nallow) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t tl = min(kTile, n - tb);
-    TileFlags fl;
-    fl.valid = (1u << (kVec * 4)) - 1u;
-    if (tl < kTile) {  // the row's last, partial tile
-        fl.valid = 0;
+    uint32_t valid = (1u << (kVec * 4)) - 1u;
+    if (tb + kTile > n) {  // the row's last, partial tile
+        valid = 0;
 #pragma unroll
         for (int e = 0; e < kVec * 4; e++)
-            if (4u * ((e >> 2) * kBlock + tid) + (e & 3) < tl) fl.valid |= 1u << e;
+            if (tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3) < n) valid |= 1u << e;
     }
-    if (m.logprobs) {
+    // bitmap words first: their LDS latency overlaps the exponentials (words
+    // past the row are read, in bounds, and masked off below)
+    uint32_t bw[kVec];
+#pragma unroll
+    for (int j = 0; j < kVec; j++) bw[j] = pen_lookup ? lds_bitmap()[(tb + 4u * (j * kBlock + tid)) >> 5] : 0u;
+    if (logprobs) {
         float sum = 0.0f;
 #pragma unroll
         for (int e = 0; e < kVec * 4; e++)
-            sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
+            sum += __builtin_amdgcn_exp2f(__builtin_fmaf(v[e >> 2][e & 3], kL2E, L.nl));
         if (!(sum < 0x1p100f)) {
-            float tmax = lref;
+            float tmax = L.ref;
 #pragma unroll
             for (int e = 0; e < kVec * 4; e++) tmax = fmaxf(tmax, v[e >> 2][e & 3]);
-            lsum *= exp2(static_cast<double>(lref - tmax) * 1.4426950408889634);
-            lref = tmax;
+            L.sum *= exp2(static_cast<double>(L.ref - tmax) * 1.4426950408889634);
+            L.set_ref(tmax);
             sum = 0.0f;
 #pragma unroll
             for (int e = 0; e < kVec * 4; e++)
-                sum += __builtin_amdgcn_exp2f((v[e >> 2][e & 3] - lref) * 1.44269504088896341f);
+                sum += __builtin_amdgcn_exp2f(__builtin_fmaf(v[e >> 2][e & 3], kL2E, L.nl));
         }
-        lsum += static_cast<double>(sum);
+        L.sum += static_cast<double>(sum * L.corr);
     }
-    fl.pen = 0;
-    fl.al = 0;
-    uint32_t* misc = lds_misc();
-    uint2* pen = lds_pen();
+    uint32_t pen = 0, al = 0;
 #pragma unroll
     for (int j = 0; j < kVec; j++) {
-        const uint32_t id0 = tb + 4u * (j * kBlock + tid);
-        if (m.penal && fast_hist && id0 < n) {
-            const uint32_t bits4 = (lds_bitmap()[id0 >> 5] >> (id0 & 31u)) & 0xFu;  // 4 ids of one word
-            if (bits4) {
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    if (((bits4 >> q) & 1u) && id0 + q < n) {
-                        const float x = v[j][q];
-                        v[j][q] = penalize(x, history_count(id0 + q), m, P);
-                        fl.pen |= 1u << (j * 4 + q);
-                        if (track_pen) {
-                            const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
-                            if (pos < kPenCap) pen[pos] = make_uint2(__float_as_uint(x), id0 + q);
-                        }
-                    }
-                }
-            }
-        }
-        if (m.constrained) fl.al |= ((mw[j] >> (id0 & 31u)) & 0xFu) << (j * 4);
+        const uint32_t sh = (tb + 4u * (j * kBlock + tid)) & 31u;
+        pen |= ((bw[j] >> sh) & 0xFu) << (j * 4);
+        if (constrained) al |= ((mw[j] >> sh) & 0xFu) << (j * 4);
     }
-    fl.al &= fl.valid;
-    nallow += __popc(fl.al);
+    pen &= valid;
+    al &= valid;
+    nallow += __popc(al);
+    if (track_pen && pen) {
+        // static element indices: an indexed read of v would put the tile in
+        // scratch memory, whose accesses wait on the prefetch loads
+        uint32_t* misc = lds_misc();
+#pragma unroll
+        for (int e = 0; e < kVec * 4; e++)
+            if ((pen >> e) & 1u) {
+                const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
+                if (pos < kPenCap)
+                    lds_pen()[pos] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
+                                                tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3u));
+            }
+    }
+    TileFlags fl;
+    fl.elig = valid & ~pen;
+    fl.valid = valid;
+    fl.pen = pen;
+    fl.al = al;
     return fl;
+}
+
+// Histogram shift that puts a span of keys into at most 256 bins.
+__device__ __forceinline__ uint32_t geo_shift(uint32_t base, uint32_t top) {
+    const uint32_t span = top > base ? top - base : 0u;
+    const int bits = 32 - __clz(static_cast<int>(span));
+    return bits > 8 ? static_cast<uint32_t>(bits - 8) : 0u;
+}
+
+// Stream candidate test of element e after the first tile: at or above the
+// all / raw threshold, or allowed and at or above the allowed threshold (only
+// compared when it is the lower one: kL), and inside the row (only checked in
+// the row's last tile: kTail).  Penalized ids pass on their raw value here;
+// their entries carry kEntPen and are dropped when the segments are closed
+// up (their penalized values join at the end).
+template <bool kL, bool kTail>
+__device__ __forceinline__ bool stream_cand(const float (&v)[kVec][4], int e, const TileFlags& fl, float tAR,
+                                            float tL) {
+    const float y = v[e >> 2][e & 3];
+    bool k = y >= tAR;
+    if (kL) k = static_cast<bool>(k | (static_cast<bool>((fl.al >> e) & 1u) & (y >= tL)));
+    if (kTail) k = static_cast<bool>(k & static_cast<bool>((fl.valid >> e) & 1u));
+    return k;
+}
+
+// Candidates of this wave in one tile (uniform).
+template <bool kL, bool kTail>
+__device__ __forceinline__ uint32_t stream_count(const float (&v)[kVec][4], const TileFlags& fl, float tAR, float tL) {
+    uint32_t tot = 0;
+#pragma unroll
+    for (int e = 0; e < kVec * 4; e++)
+        tot += static_cast<uint32_t>(__popcll(wave_ballot(stream_cand<kL, kTail>(v, e, fl, tAR, tL))));
+    return tot;
+}
+
+// Writes this wave's candidates of one tile from buffer index pos on, in
+// element-slot order (a slot's lanes in lane order, placed by their ballot).
+template <bool kL, bool kTail>
+__device__ __forceinline__ void stream_write(const float (&v)[kVec][4], const TileFlags& fl, float tAR, float tL,
+                                             uint32_t pos, uint32_t tb) {
+    const uint32_t tid = threadIdx.x;
+    uint2* buf = lds_buf();
+#pragma unroll
+    for (int e = 0; e < kVec * 4; e++) {
+        const bool k = stream_cand<kL, kTail>(v, e, fl, tAR, tL);
+        const uint64_t b = wave_ballot(k);
+        if (b == 0) continue;
+        if (k)
+            buf[pos + lanes_below(b)] =
+                make_entry(v[e >> 2][e & 3], tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3), fl.pen, fl.al, e);
+        pos += static_cast<uint32_t>(__popcll(b));
+    }
 }
 
 // After the streaming pass: logsumexp and allowed count, then the pick (or
@@ -594,21 +745,21 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
     const uint2* pen = lds_pen();
 
     // ---------------- row statistics ----------------
-    __syncthreads();
+    TSM_LDS_SYNC();
     {
         const uint32_t wal = wave_sum(nallow);
         if (lane_id() == 0) tmp[tid / kWave] = wal;
-        __syncthreads();
+        TSM_LDS_SYNC();
         uint32_t al = 0;
         for (int w = 0; w < kBlock / kWave; w++) al += tmp[w];
         nallow = al;
-        __syncthreads();
+        TSM_LDS_SYNC();
     }
     const uint32_t flags = misc[M_FLAGS];
     const uint32_t penn = misc[M_PENN];
     const bool buf_ok = !(flags & (ROWF_BUF_OVERFLOW | ROWF_SLOW_HISTORY));
     const bool raw_ok = buf_ok && penn <= kPenCap && tg0.need[SK_RAW] > 0;
-    __syncthreads();
+    TSM_LDS_SYNC();
     // the best raw logit (value desc, id asc): the raw argmax and the max of
     // the logsumexp, from the buffer's non-penalized entries and the
     // penalized list, or by re-reading the row
@@ -636,10 +787,10 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
             }
             unsigned long long* wb = reinterpret_cast<unsigned long long*>(lds_miscd() + 8);
             if (lane_id() == 0) wb[tid / kWave] = best;
-            __syncthreads();
+            TSM_LDS_SYNC();
             unsigned long long all = ~0ull;
             for (int w = 0; w < kBlock / kWave; w++) all = wb[w] < all ? wb[w] : all;
-            __syncthreads();
+            TSM_LDS_SYNC();
             raw_best = all;
         } else {
             Filt q;
@@ -655,11 +806,11 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
         part = wave_sum(part);
         double* wsum = lds_miscd() + 16;  // 16 doubles
         if (lane_id() == 0) wsum[tid / kWave] = part;
-        __syncthreads();
+        TSM_LDS_SYNC();
         double rs = 0.0;
         for (int w = 0; w < kBlock / kWave; w++) rs += wsum[w];
         lse = rmax + static_cast<float>(log(rs));
-        __syncthreads();
+        TSM_LDS_SYNC();
     }
 
     // ---------------- finish ----------------
@@ -698,7 +849,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
         // the ranked list from the buffer
         uint64_t* gcomp = f.gcomp();
         if (tid == 0) misc[M_CNT] = 0;
-        __syncthreads();
+        TSM_LDS_SYNC();
         const bool constrained = m.constrained;
         for (uint32_t i = tid; i < bufn; i += kBlock) {
             const uint2 e = buf[i];
@@ -708,9 +859,9 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
                 if (pos < kExactCap) gcomp[pos] = c;
             }
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
         uint32_t g = min(misc[M_CNT], kExactCap);
-        __syncthreads();
+        TSM_LDS_SYNC();
         uint32_t len = 0;
         if (g > 0) {
             sort_gathered(f, g);
@@ -719,7 +870,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
             // no allowed id in the window: the whole-vocabulary fallback
             // (sampler.rs:211-221), ordered by f32::total_cmp
             if (tid == 0) misc[M_CNT] = 0;
-            __syncthreads();
+            TSM_LDS_SYNC();
             for (uint32_t i = tid; i < bufn; i += kBlock) {
                 const uint2 e = buf[i];
                 if (!(e.y & kEntAllowed)) continue;
@@ -729,9 +880,9 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
                     if (pos < kExactCap) gcomp[pos] = c;
                 }
             }
-            __syncthreads();
+            TSM_LDS_SYNC();
             g = min(misc[M_CNT], kExactCap);
-            __syncthreads();
+            TSM_LDS_SYNC();
             sort_gathered(f, g);
             len = min(g, m.want);
         }
@@ -760,7 +911,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
         uint32_t nraw;
         if (raw_ok && sel.T[SK_RAW] != ~0ull) {
             if (tid == 0) misc[M_CNT] = 0;
-            __syncthreads();
+            TSM_LDS_SYNC();
             for (uint32_t i = tid; i < bufn; i += kBlock) {
                 const uint2 e = buf[i];
                 if (e.y & kEntPen) continue;
@@ -778,9 +929,9 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
                     if (pos < kExactCap) gcomp[pos] = c;
                 }
             }
-            __syncthreads();
+            TSM_LDS_SYNC();
             const uint32_t g = min(misc[M_CNT], kExactCap);
-            __syncthreads();
+            TSM_LDS_SYNC();
             sort_u64(gcomp, g);
             nraw = min(g, nlp);
         } else {
@@ -838,9 +989,9 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     tg.need[SK_ALLOWED] = (m.topk && m.constrained && fast_hist) ? m.want : 0u;
     Targets tg0 = tg;
     if (!fast_hist) tg0.need[SK_RAW] = 0u;
-    const bool track_pen = tg.need[SK_RAW] > 0 && m.penal;
-
     const bool tracking = (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
+    const bool pen_lookup = m.penal && fast_hist;  // the stream sees which ids are penalized
+    const bool track_pen = pen_lookup && tracking;  // and lists them with their raw values
     if (tid == 0) {
         misc[M_BUFN] = 0;
         misc[M_PENN] = 0;
@@ -848,40 +999,48 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         misc[M_FLAGS] = fast_hist ? 0u : ROWF_SLOW_HISTORY;
         for (int g = 0; g < 3; g++) misc[M_THR + g] = tg.need[g] ? kKeyNegInf : kKeyUntracked;
     }
-    if (tracking)  // first used after the first tile's barriers
-        for (uint32_t i = tid; i < 3 * kSBins; i += kBlock) lds_shist()[i] = 0;
-    // tiles t+1 and t+2 are in flight while tile t is processed
-    float v[kVec][4], vn[kVec][4], vn2[kVec][4];
-    uint32_t mw[kVec], mwn[kVec], mwn2[kVec];
-    load_tile<kVecLoads>(rowp, mrow, 0, n, v, mw);             // in flight while the lookup is built
-    if (kTile < n) load_tile<kVecLoads>(rowp, mrow, kTile, n, vn, mwn);
-    if (m.penal && fast_hist) history_build(f.hist, hlen, n);  // barriers inside
+    if (tracking) {  // first used after the first tile's barriers
+        for (uint32_t i = tid; i < 2 * kSBins; i += kBlock) lds_shist()[i] = 0;
+        if (tid < 2 * (kBlock / kWave)) lds_seg_pub()[tid] = 0;  // published and counted fills
+    }
+    // three register sets take the tiles in turn (tile t in set t mod 3):
+    // tiles t+1 and t+2 are in flight while tile t is processed, and no set is
+    // ever copied to another (a copy would wait for its loads)
+    float v[kVec][4], vB[kVec][4], vC[kVec][4];
+    uint32_t mw[kVec], mwB[kVec], mwC[kVec];
+    // the mask words are read unconditionally, from the logits when there is no mask
+    const uint32_t* mp = mrow ? mrow : reinterpret_cast<const uint32_t*>(rowp);
+    // (loads past the row's last tile read in bounds and go unused: an
+    // unconditional load keeps one code path)
+    load_tile<kVecLoads>(rowp, mp, 0, n, v, mw);  // in flight while the lookup is built
+    load_tile<kVecLoads>(rowp, mp, kTile, n, vB, mwB);
+    if (pen_lookup) history_build(f.hist, hlen, n);  // barriers inside
 
     SHist sh;
-#pragma unroll
-    for (int g = 0; g < 3; g++) {
-        sh.base[g] = kKeyUntracked;
-        sh.shift[g] = 0;
-    }
+    sh.base[0] = sh.base[1] = kKeyUntracked;
+    sh.shift[0] = sh.shift[1] = 0;
     bool wave_track = tracking;  // uniform per wave; cleared once the buffer overflows
     const uint32_t wid = tid / kWave, lane = lane_id();
+    // buffer segments: the first tile's entries fill [0, seg0), then each wave
+    // owns seg_cap entries; seg_fill is this wave's fill (uniform in the wave)
+    uint32_t seg0 = 0, seg_cap = 0, seg_fill = 0;
 
     // ---------------- streaming pass ----------------
-    double lsum = 0.0;  // sum of exp(x - lref) over this thread's ids
-    float lref = 0.0f;
+    LseAcc lse;
+    mask_tail(v, 0, n);
     if (m.logprobs) {
         float t0 = -INFINITY;
 #pragma unroll
         for (int e = 0; e < kVec * 4; e++) t0 = fmaxf(t0, v[e >> 2][e & 3]);
-        lref = t0 == -INFINITY ? 0.0f : t0;
+        lse.set_ref(t0 == -INFINITY ? 0.0f : t0);
     }
     uint32_t nallow = 0;
     const uint32_t ntiles = (n + kTile - 1) / kTile;
-    if (2 < ntiles) load_tile<kVecLoads>(rowp, mrow, 2 * kTile, n, vn2, mwn2);  // prefetch
+    load_tile<kVecLoads>(rowp, mp, 2 * kTile, n, vC, mwC);  // prefetch
     {
         // first tile: block-wide, so the thresholds can start from the tile's
         // own group-max bounds
-        const TileFlags fl = tile_prep(v, mw, 0, n, m, P, fast_hist, track_pen, lref, lsum, nallow);
+        const TileFlags fl = tile_prep(v, mw, 0, n, m.logprobs, pen_lookup, track_pen, m.constrained, lse, nallow);
         if (tracking) {
             float th[3];
 #pragma unroll
@@ -889,7 +1048,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             uint32_t emit = 0, total = 0, pos0 = 0;
             bool bound = ntiles > 1;
             if (!bound) {
-                emit = emit_mask(th[0], th[1], th[2], v, fl.valid, fl.pen, fl.al);
+                emit = emit_mask(fminf(th[SK_ALL], th[SK_RAW]), th[SK_ALLOWED], v, fl.elig, fl.al);
                 pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
                 bound = total > kBufCap;
             }
@@ -897,24 +1056,39 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                 uint32_t k[3] = {0u, 0u, 0u};
 #pragma unroll
                 for (int e = 0; e < kVec * 4; e++) {
-                    if (!((fl.valid >> e) & 1u)) continue;
+                    if (!((fl.elig >> e) & 1u)) continue;
                     const float y = v[e >> 2][e & 3];
                     k[SK_ALL] = max(k[SK_ALL], canon_key(y));
-                    if (!((fl.pen >> e) & 1u)) k[SK_RAW] = max(k[SK_RAW], canon_key(y));
                     if ((fl.al >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
                 }
+                k[SK_RAW] = k[SK_ALL];  // the stream's candidates are the non-penalized ids
                 uint32_t top[3];
                 tile_bounds(tg, k[0], k[1], k[2], top);
+                uint32_t key[3];
 #pragma unroll
                 for (int g = 0; g < 3; g++) {
-                    const uint32_t b = misc[M_THR + g];
-                    th[g] = thr_float(b);
-                    sh.base[g] = b;
-                    const uint32_t span = top[g] > b ? top[g] - b : 0u;
-                    const int bits = 32 - __clz(span);
-                    sh.shift[g] = bits > 8 ? static_cast<uint32_t>(bits - 8) : 0u;
+                    key[g] = misc[M_THR + g];
+                    th[g] = thr_float(key[g]);
                 }
-                emit = emit_mask(th[0], th[1], th[2], v, fl.valid, fl.pen, fl.al);
+                // histogram geometry: H[0] from the all / raw bounds; H[1] from
+                // the allowed bound, or H[0]'s when the first tile gave none
+                uint32_t b0 = kKeyUntracked, t0 = 0;
+#pragma unroll
+                for (int g = 0; g < 2; g++)
+                    if (tg.need[g]) {
+                        b0 = min(b0, key[g]);
+                        t0 = max(t0, top[g]);
+                    }
+                sh.base[0] = b0;
+                sh.shift[0] = geo_shift(b0, t0);
+                if (tg.need[SK_ALLOWED] && key[SK_ALLOWED] > kKeyNegInf) {
+                    sh.base[1] = key[SK_ALLOWED];
+                    sh.shift[1] = geo_shift(key[SK_ALLOWED], top[SK_ALLOWED]);
+                } else {
+                    sh.base[1] = sh.base[0];
+                    sh.shift[1] = sh.shift[0];
+                }
+                emit = emit_mask(fminf(th[SK_ALL], th[SK_RAW]), th[SK_ALLOWED], v, fl.elig, fl.al);
                 pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
             }
             if (total > kBufCap) {  // uniform: stop tracking, the finish re-reads
@@ -928,85 +1102,170 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             for (int e = 0; e < kVec * 4; e++)
                 if ((emit >> e) & 1u) {
                     const float y = v[e >> 2][e & 3];
-                    buf[pos++] = make_entry(y, 4u * ((e >> 2) * kBlock + tid) + (e & 3), fl.pen, fl.al, e);
-                    if (bound) count_kept(y, (fl.pen >> e) & 1u, (fl.al >> e) & 1u, th[0], th[1], th[2], sh);
+                    buf[pos++] = make_entry(y, 4u * ((e >> 2) * kBlock + tid) + (e & 3), 0u, fl.al, e);
+                    if (bound) count_kept(y, (fl.al >> e) & 1u, sh);
                 }
-            if (tid == 0) misc[M_BUFN] = total;
-            __syncthreads();
-        }
-#pragma unroll
-        for (int j = 0; j < kVec; j++) {
-            mw[j] = mwn[j];
-            mwn[j] = mwn2[j];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                v[j][q] = vn[j][q];
-                vn[j][q] = vn2[j][q];
-            }
+            seg0 = total;
+            seg_cap = ((kBufCap - total) / (kBlock / kWave)) & ~1u;
+            TSM_LDS_SYNC();
         }
     }
-    for (uint32_t t = 1; t < ntiles; t++) {
+    // tile t (>= 1) in register set v, the prefetch of tile t+2 into set pf
+    auto step = [&](const uint32_t t, float (&v)[kVec][4], const uint32_t (&mw)[kVec], float (&pf)[kVec][4],
+                    uint32_t (&mpf)[kVec]) __attribute__((always_inline)) {
         const uint32_t tb = t * kTile;
-        if (t + 2 < ntiles) load_tile<kVecLoads>(rowp, mrow, tb + 2 * kTile, n, vn2, mwn2);  // prefetch
-        const TileFlags fl = tile_prep(v, mw, tb, n, m, P, fast_hist, track_pen, lref, lsum, nallow);
-        // candidates at or above the thresholds as they are now (they only
-        // rise, so any value read is valid); no barriers: each wave reserves
-        // its slots with one LDS atomic
-        if (wave_track && wave_uniform(lds_load_relaxed(&misc[M_OVF])) != 0u)
-            wave_track = false;  // the buffer overflowed: the finish re-reads the row
+        load_tile<kVecLoads>(rowp, mp, tb + 2 * kTile, n, pf, mpf);
+        mask_tail(v, tb, n);
+        // the thresholds as they are now (they only rise, so any value read is
+        // valid), loaded before the tile's arithmetic so it hides their latency
+        uint32_t ovf = 0, kA = 0, kR = 0, kL = 0;
         if (wave_track) {
-            const float tA = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)])));
-            const float tR = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)])));
-            const float tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
-            const float tmin = fminf(tA, fminf(tR, tL));
-            float mx = v[0][0];
+            ovf = lds_load_relaxed(&misc[M_OVF]);
+            kA = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)]);
+            kR = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]);
+            kL = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)]);
+        }
+        const TileFlags fl = tile_prep(v, mw, tb, n, m.logprobs, pen_lookup, track_pen, m.constrained, lse, nallow);
+        if (wave_track && wave_uniform(ovf) != 0u) wave_track = false;  // the finish re-reads the row
+        if (wave_track) {
+            // no barriers: each wave appends to its own segment and publishes
+            // the segment's fill
+            const bool tail = tb + kTile > n;
+            float tAR = fminf(thr_float(wave_uniform(kA)), thr_float(wave_uniform(kR)));
+            float tL = thr_float(wave_uniform(kL));
+            bool use_l = !(tL >= tAR) && tL == tL;  // allowed ids need a compare of their own
+            auto count = [&]() __attribute__((always_inline)) {
+                return use_l ? (tail ? stream_count<true, true>(v, fl, tAR, tL) : stream_count<true, false>(v, fl, tAR, tL))
+                             : (tail ? stream_count<false, true>(v, fl, tAR, tL) : stream_count<false, false>(v, fl, tAR, tL));
+            };
+            uint32_t tot = count();
+            if (tot > kBigEmit) {
+                // far more candidates than a tile should bring (a target the
+                // first tile could not bound, or a dense stretch of the row):
+                // raise the thresholds from this wave's own lane maxima, then
+                // keep what still passes
+                uint32_t lmA = 0, lmL = 0;
 #pragma unroll
-            for (int e = 1; e < kVec * 4; e++) mx = fmaxf(mx, v[e >> 2][e & 3]);
-            if (wave_ballot(mx >= tmin) != 0) {
-                const uint32_t emit = emit_mask(tA, tR, tL, v, fl.valid, fl.pen, fl.al);
-                const uint32_t cnt = __popc(emit);
-                const uint32_t incl = wave_incl_scan(cnt);
-                const uint32_t wtot = wave_read(incl, kWave - 1);
-                if (wtot) {
-                    uint32_t base = 0;
-                    if (lane == kWave - 1) base = atomicAdd(&misc[M_BUFN], wtot);
-                    base = wave_read(base, kWave - 1);
-                    if (base + wtot <= kBufCap) {
-                        uint32_t pos = base + incl - cnt;
-#pragma unroll
-                        for (int e = 0; e < kVec * 4; e++)
-                            if ((emit >> e) & 1u) {
-                                const float y = v[e >> 2][e & 3];
-                                const uint32_t id = tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3);
-                                buf[pos++] = make_entry(y, id, fl.pen, fl.al, e);
-                                count_kept(y, (fl.pen >> e) & 1u, (fl.al >> e) & 1u, tA, tR, tL, sh);
-                            }
-                    } else if (lane == 0) {
-                        atomicOr(&misc[M_OVF], 1u);
+                for (int e = 0; e < kVec * 4; e++)
+                    if ((fl.elig >> e) & 1u) {
+                        const uint32_t ck = canon_key(v[e >> 2][e & 3]);
+                        lmA = max(lmA, ck);
+                        if ((fl.al >> e) & 1u) lmL = max(lmL, ck);
                     }
+#pragma unroll
+                for (int g = 0; g < 3; g++) {
+                    const uint32_t need = tg.need[g];
+                    if (need == 0 || need > static_cast<uint32_t>(kWave)) continue;
+                    const uint32_t kb = wave_lane_bound(g == SK_ALLOWED ? lmL : lmA, need);
+                    if (kb != 0u && lane == 0) atomicMax(&misc[M_THR + g], kb);
+                }
+                tAR = fminf(thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)]))),
+                            thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]))));
+                tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
+                use_l = !(tL >= tAR) && tL == tL;
+                tot = count();
+            }
+            if (tot) {
+                if (seg_fill + tot <= seg_cap) {
+                    const uint32_t pos = seg0 + wid * seg_cap + seg_fill;
+                    if (use_l) {
+                        if (tail) stream_write<true, true>(v, fl, tAR, tL, pos, tb);
+                        else stream_write<true, false>(v, fl, tAR, tL, pos, tb);
+                    } else {
+                        if (tail) stream_write<false, true>(v, fl, tAR, tL, pos, tb);
+                        else stream_write<false, false>(v, fl, tAR, tL, pos, tb);
+                    }
+                    // the fill each lane publishes covers every lane's entries:
+                    // all lanes' writes come before any lane's publish
+                    __builtin_amdgcn_wave_barrier();
+                    seg_fill += tot;
+                    lds_publish_max(&lds_seg_pub()[wid], seg_fill);
+                } else {
+                    if (lane == 0) atomicOr(&misc[M_OVF], 1u);
+                    wave_track = false;
                 }
             }
-            if (wid == (t & (kBlock / kWave - 1))) raise_thresholds(tg, sh);
-        }
-#pragma unroll
-        for (int j = 0; j < kVec; j++) {
-            mw[j] = mwn[j];
-            mwn[j] = mwn2[j];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                v[j][q] = vn[j][q];
-                vn[j][q] = vn2[j][q];
+            // one wave counts what was published and raises the thresholds:
+            // every tile at first, every second tile later on
+            if (wave_track && wid == (t & (kBlock / kWave - 1)) && (t < 8 || (t & 1u) == 0)) {
+                count_published(sh, seg0, seg_cap);
+                raise_thresholds(tg, sh);
             }
         }
+    };
+    for (uint32_t t = 1; t < ntiles; t += 3) {
+        step(t, vB, mwB, v, mw);
+        if (t + 1 >= ntiles) break;
+        step(t + 1, vC, mwC, vB, mwB);
+        if (t + 2 >= ntiles) break;
+        step(t + 2, v, mw, vC, mwC);
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     uint32_t bufn = 0;
     if (tracking) {
+        // the stream's final state, read by every thread before anything below
+        // changes it (the decisions taken from it must be uniform)
+        const uint32_t ovf0 = misc[M_OVF], penn0 = misc[M_PENN];
+        const float tA = thr_float(misc[M_THR + static_cast<uint32_t>(SK_ALL)]);
+        const float tL = thr_float(misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)]);
+        // close up the wave segments behind the first tile's entries, dropping
+        // the entries of penalized ids (their penalized values join below):
+        // each wave holds its entries in registers across the barrier, then
+        // writes the kept ones at its place
+        constexpr uint32_t kSegRegs = kBufCap / (kBlock / kWave) / kWave;
+        const uint32_t mine = ovf0 ? 0u : lds_seg_pub()[wid];
+        uint2 held[kSegRegs];
+        bool kept[kSegRegs];
+        uint32_t kept_w = 0;  // uniform
+#pragma unroll
+        for (uint32_t k = 0; k < kSegRegs; k++) {
+            const uint32_t i = lane + k * kWave;
+            kept[k] = false;
+            if (i < mine) {
+                held[k] = buf[seg0 + wid * seg_cap + i];
+                kept[k] = !(held[k].y & kEntPen);
+            }
+            kept_w += static_cast<uint32_t>(__popcll(wave_ballot(kept[k])));
+        }
+        if (lane == 0) lds_tmp()[wid] = kept_w;
+        TSM_LDS_SYNC();
+        uint32_t before = 0, fill0 = seg0;
+        for (uint32_t w = 0; w < kBlock / kWave; w++) {
+            const uint32_t c = lds_tmp()[w];
+            before += w < wid ? c : 0u;
+            fill0 += c;
+        }
+        uint32_t dst = seg0 + before;
+#pragma unroll
+        for (uint32_t k = 0; k < kSegRegs; k++) {
+            const uint64_t b = wave_ballot(kept[k]);
+            if (kept[k]) buf[dst + lanes_below(b)] = held[k];
+            dst += static_cast<uint32_t>(__popcll(b));
+        }
+        if (tid == 0) misc[M_BUFN] = fill0;
+        TSM_LDS_SYNC();
+        // penalized ids join the candidates when their penalized value passes
+        // the final thresholds (every element at or above them is then in the
+        // buffer)
+        if (track_pen && ovf0 == 0u && fill0 <= kBufCap) {
+            const uint32_t penn = min(penn0, kPenCap);
+            for (uint32_t i = tid; i < penn; i += kBlock) {
+                const uint2 e = pen[i];
+                const uint32_t id = e.y;
+                const float y = penalize(__uint_as_float(e.x), history_count(id), m, P);
+                const bool al = m.constrained && ((mrow[id >> 5] >> (id & 31u)) & 1u);
+                if (keep2(y, al, tA, tL)) {
+                    const uint32_t pos = atomicAdd(&misc[M_BUFN], 1u);
+                    if (pos < kBufCap) buf[pos] = make_uint2(__float_as_uint(y), id | kEntPen | (al ? kEntAllowed : 0u));
+                }
+            }
+            TSM_LDS_SYNC();
+        }
         const uint32_t fill = misc[M_BUFN];
         if (tid == 0 && (fill > kBufCap || misc[M_OVF] != 0u)) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
         bufn = min(fill, kBufCap);
     }
-    finish_row(a, f, tg0, nlp, lref, lsum, nallow, bufn);
+    finish_row(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn);
 }
 
 template __global__ void sample_kernel<true>(SampleArgs);

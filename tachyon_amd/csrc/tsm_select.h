@@ -43,8 +43,9 @@ constexpr uint32_t kOffMisc = kOffPen + kPenCap * 8;             // u32[64]
 constexpr uint32_t kOffMiscD = kOffMisc + 64 * 4;                // f64[32]
 constexpr uint32_t kOffTmp = kOffMiscD + 32 * 8;                 // u32[64] scan scratch
 constexpr uint32_t kSBins = 512;                                 // stream histogram bins per threshold
-constexpr uint32_t kOffSHist = kOffTmp + 64 * 4;                 // 3 x u32[kSBins]
-constexpr uint32_t kSmem = kOffSHist + 3 * kSBins * 4;
+constexpr uint32_t kOffSHist = kOffTmp + 64 * 4;                 // 2 x u32[kSBins]
+constexpr uint32_t kOffSeg = kOffSHist + 2 * kSBins * 4;         // per wave: published fill, counted fill
+constexpr uint32_t kSmem = kOffSeg + 2 * (kBlock / kWave) * 4;
 static_assert(kOffGather % 8 == 0 && (kOffHist + kBins * 4) % 8 == 0 && kOffBuf % 8 == 0 && kOffPen % 8 == 0 &&
                   kOffMiscD % 8 == 0,
               "u64 / f64 LDS records are 8-byte aligned");
@@ -140,15 +141,15 @@ __device__ void row_pass(Fin& f, F&& fn) {
     for (uint32_t tb = 0; tb < f.n; tb += kReTile) {
         const uint32_t tl = min(kReTile, f.n - tb);
         if (f.m.penal) {
-            __syncthreads();
+            TSM_LDS_SYNC();
             for (uint32_t i = tid; i < kReTile / 2; i += kBlock) f.cnt()[i] = 0;
-            __syncthreads();
+            TSM_LDS_SYNC();
             const uint32_t hc = min(f.hlen, TSM_MAX_HISTORY);
             for (uint32_t h = tid; h < hc; h += kBlock) {
                 const uint32_t li = f.hist[h] - tb;
                 if (li < tl) atomicAdd(&f.cnt()[li >> 1], 1u << ((li & 1u) << 4));
             }
-            __syncthreads();
+            TSM_LDS_SYNC();
         }
         for (uint32_t i = tid; i < tl; i += kBlock) {
             const uint32_t id = tb + i;
@@ -161,7 +162,7 @@ __device__ void row_pass(Fin& f, F&& fn) {
             fn(id, x, y);
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 // Block-wide bitonic sort, ascending, of n u64 (n a power of two <= 4096).
@@ -179,7 +180,7 @@ __device__ void bitonic_sort(uint64_t* a, uint32_t n) {
                     }
                 }
             }
-            __syncthreads();
+            TSM_LDS_SYNC();
         }
 }
 
@@ -215,7 +216,7 @@ __device__ uint64_t select_from(Fin& f, const Filt& q, uint32_t need, int r0, ui
         const int lo = kRoundLo[r], w = kRoundW[r];
         for (uint32_t i = tid; i < kBins; i += kBlock) f.hcnt()[i] = 0;
         if (tid < 2) f.misc()[M_FIND + tid] = 0xFFFFFFFFu;
-        __syncthreads();
+        TSM_LDS_SYNC();
         const uint64_t kn = known;
         const int kl = known_lo;
         row_pass(f, [&](uint32_t id, float x, float y) {
@@ -228,7 +229,7 @@ __device__ uint64_t select_from(Fin& f, const Filt& q, uint32_t need, int r0, ui
         if (d == 0xFFFFFFFFu) return ~0ull;
         const uint32_t before = f.misc()[M_FIND + 1];
         const uint32_t binc = f.hcnt()[d];
-        __syncthreads();
+        TSM_LDS_SYNC();
         known |= static_cast<uint64_t>(d) << lo;
         known_lo = lo;
         need -= before;
@@ -262,10 +263,10 @@ __device__ uint64_t exact_at(Fin& f, const Filt& q, uint64_t T) {
     }
     unsigned long long* wtmp = reinterpret_cast<unsigned long long*>(f.miscd() + 8);
     if ((threadIdx.x & (kWave - 1)) == 0) wtmp[threadIdx.x / kWave] = best;
-    __syncthreads();
+    TSM_LDS_SYNC();
     unsigned long long all = 0;
     for (int w = 0; w < kBlock / kWave; w++) all = wtmp[w] > all ? wtmp[w] : all;
-    __syncthreads();
+    TSM_LDS_SYNC();
     return all == 0 ? ~0ull : all - 1ull;
 }
 
@@ -280,14 +281,14 @@ __device__ double block_excl_scan_f64(double v, double* tmp, double* total) {
         if (lane >= o) inc += w;
     }
     if (lane == kWave - 1) tmp[wid] = inc;
-    __syncthreads();
+    TSM_LDS_SYNC();
     double before = 0.0, all = 0.0;
     for (int w = 0; w < NW; w++) {
         const double t = tmp[w];
         if (w < wid) before += t;
         all += t;
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     *total = all;
     return before + inc - v;
 }
@@ -317,7 +318,7 @@ __device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
             f.misc()[M_FIND] = 0xFFFFFFFFu;
             f.misc()[M_FIND2] = 0;
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
         const uint64_t kn = known;
         const int kl = known_lo;
         row_pass(f, [&](uint32_t id, float x, float y) {
@@ -342,7 +343,7 @@ __device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
         else if (c1 > 0 && base + m0 + m1 >= target) cand = b0 + 1;
         if (cand != 0xFFFFFFFFu) atomicMin(&f.misc()[M_FIND], cand);
         if (c0 + c1 > 0) atomicMax(&f.misc()[M_FIND2], (c1 > 0 ? b0 + 1 : b0) + 1);  // last nonempty + 1
-        __syncthreads();
+        TSM_LDS_SYNC();
         uint32_t d = f.misc()[M_FIND];
         const bool overshoot = d == 0xFFFFFFFFu;  // read now: select_from below rewrites M_FIND
         if (overshoot) d = f.misc()[M_FIND2] - 1;   // target beyond the total: last element
@@ -352,13 +353,13 @@ __device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
             f.misc()[M_CNT] = cb + (second ? c0 : 0u);
             f.misc()[M_TOTAL] = second ? c1 : c0;
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
         cum_before = f.miscd()[0];
         cnt_before += f.misc()[M_CNT];
         const uint32_t ties = f.misc()[M_TOTAL];
         known |= static_cast<uint64_t>(d) << lo;
         known_lo = lo;
-        __syncthreads();
+        TSM_LDS_SYNC();
         if (r == 2) {
             // key resolved: all `ties` elements share one value and one p
             const uint32_t key = ~static_cast<uint32_t>(known >> 32);
@@ -392,7 +393,7 @@ __device__ double mass_total(Fin& f, const Filt& q, float y0) {
 // Gathers filtered elements' composites into gcomp (caller guarantees <= cap).
 __device__ uint32_t gather_pass(Fin& f, const Filt& q, uint32_t cap) {
     if (threadIdx.x == 0) f.misc()[M_CNT] = 0;
-    __syncthreads();
+    TSM_LDS_SYNC();
     row_pass(f, [&](uint32_t id, float x, float y) {
         const uint64_t c = comp_of(q.order, id, x, y);
         if (keep_el(f, q, id, y, c)) {
@@ -401,7 +402,7 @@ __device__ uint32_t gather_pass(Fin& f, const Filt& q, uint32_t cap) {
         }
     });
     const uint32_t n = min(f.misc()[M_CNT], cap);
-    __syncthreads();
+    TSM_LDS_SYNC();
     return n;
 }
 
@@ -423,12 +424,12 @@ __device__ void sort_u64(uint64_t* a, uint32_t n) {
                 }
             if (tid < n) a[tid] = v;
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
         return;
     }
     const uint32_t n2 = pow2_ceil(n);
     for (uint32_t i = n + tid; i < n2; i += kBlock) a[i] = ~0ull;
-    __syncthreads();
+    TSM_LDS_SYNC();
     bitonic_sort(a, n2);
 }
 
@@ -440,7 +441,7 @@ __device__ void sort_gathered(Fin& f, uint32_t n) {
         f.ry()[j] = key_to_float(~static_cast<uint32_t>(c >> 32));
         f.rid()[j] = static_cast<uint32_t>(c);
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
 }
 
 struct Pick {
@@ -465,11 +466,11 @@ __device__ Pick exact_finalize(Fin& f, uint32_t len, float u, bool draw) {
     const float y0 = f.ry()[0];
     for (uint32_t j = tid; j < len; j += kBlock) f.rp()[j] = glibc_expf((f.ry()[j] - y0) / f.m.t);
     if (tid == 0) f.misc()[M_FIRST] = len;
-    __syncthreads();
+    TSM_LDS_SYNC();
     if (!f.m.greedy && f.P.min_p > 0.0f) {
         for (uint32_t j = tid; j < len; j += kBlock)
             if (!(f.rp()[j] >= f.P.min_p)) atomicMin(&f.misc()[M_FIRST], j);
-        __syncthreads();
+        TSM_LDS_SYNC();
         len = max(f.misc()[M_FIRST], 1u);
     }
     const bool topp = !(f.m.greedy || f.P.top_p >= 1.0f);
@@ -487,7 +488,7 @@ __device__ Pick exact_finalize(Fin& f, uint32_t len, float u, bool draw) {
             if (lane < cnt) f.rP()[b + lane] = mine;
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     if (tid < kWave) {
         const uint32_t lane = tid;
         const float total = f.rP()[len - 1];
@@ -534,13 +535,13 @@ __device__ Pick exact_finalize(Fin& f, uint32_t len, float u, bool draw) {
             f.misc()[M_MASS] = __float_as_uint(mass);
         }
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     Pick p;
     p.token = f.misc()[M_TOKEN];
     p.keep = f.misc()[M_KEEP];
     p.prob = __uint_as_float(f.misc()[M_PROB]);
     p.mass = __uint_as_float(f.misc()[M_MASS]);
-    __syncthreads();
+    TSM_LDS_SYNC();
     return p;
 }
 
@@ -582,7 +583,7 @@ __device__ bool slow_topk_window(Fin& f, uint32_t* len) {
         f.ry()[pos] = yv;
         f.rid()[pos] = idv;
     }
-    __syncthreads();
+    TSM_LDS_SYNC();
     *len = min(total, f.m.want);
     return total > 0;
 }
@@ -659,12 +660,12 @@ __device__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* 
             ftmp[tid / 64] = la;
             ftmp[16 + tid / 64] = lb;
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
         for (int w = 0; w < kBlock / kWave; w++) {
             mall = fmaxf(mall, ftmp[w]);
             mal = fmaxf(mal, ftmp[16 + w]);
         }
-        __syncthreads();
+        TSM_LDS_SYNC();
     }
     const float cut = mall - 30.0f * m.t;  // sampler.rs:198-199
     Filt q0;
@@ -741,7 +742,7 @@ __device__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* 
         if (keep > g && tid == 0) atomicOr(dist->status, TSM_STATUS_DIST_TRUNCATED);
         pk.token = g > 0 ? f.rid()[0] : 0u;
         pk.prob = 0.0f;
-        __syncthreads();
+        TSM_LDS_SYNC();
         return pk;
     }
     const MassSel sr = mass_select(f, q3, y0, static_cast<double>(u) * mass);

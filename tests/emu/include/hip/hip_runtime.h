@@ -79,6 +79,8 @@ void run_launch(dim3 grid, dim3 block, size_t smem, const Body& body);
 #define blockDim (::emu::g_blockDim)
 #define gridDim (::emu::g_gridDim)
 #define __syncthreads() ::emu::syncthreads(__FILE__, __LINE__)
+// s_barrier: a block barrier (the kernels put their LDS fences around it)
+#define __builtin_amdgcn_s_barrier() ::emu::syncthreads(__FILE__, __LINE__)
 
 #include <type_traits>
 template <class T, class U>
@@ -163,10 +165,31 @@ inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t mask, uint32_t acc) {
     return acc + static_cast<uint32_t>(__builtin_popcount(mask & below));
 }
 #define __HIP_MEMORY_SCOPE_WORKGROUP 3
+inline std::memory_order emu_order(int order) {
+    switch (order) {
+        case __ATOMIC_RELAXED: return std::memory_order_relaxed;
+        case __ATOMIC_ACQUIRE: return std::memory_order_acquire;
+        case __ATOMIC_RELEASE: return std::memory_order_release;
+        case __ATOMIC_ACQ_REL: return std::memory_order_acq_rel;
+        default: return std::memory_order_seq_cst;
+    }
+}
+// The kernels pair relaxed LDS atomics with LDS-only fences
+// (__builtin_amdgcn_fence(..., "workgroup", "local")).  ThreadSanitizer does
+// not model standalone fences, so here the fences are no-ops and every
+// atomic load acquires and every atomic read-modify-write releases and
+// acquires: the same orderings the fence + relaxed pairs give on the GPU.
+#define __builtin_amdgcn_fence(...) ((void)0)
 template <class T>
-inline T __hip_atomic_load(T* p, int order, int) {
-    return std::atomic_ref<T>(*p).load(order == __ATOMIC_RELAXED ? std::memory_order_relaxed
-                                                                 : std::memory_order_seq_cst);
+inline T __hip_atomic_load(T* p, int, int) {
+    return std::atomic_ref<T>(*p).load(std::memory_order_acquire);
+}
+template <class T>
+inline T __hip_atomic_fetch_max(T* p, T v, int, int) {
+    std::atomic_ref<T> a(*p);
+    T old = a.load(std::memory_order_relaxed);
+    while (!a.compare_exchange_weak(old, old > v ? old : v, std::memory_order_acq_rel, std::memory_order_relaxed)) {}
+    return old;
 }
 
 template <class T>
