@@ -142,27 +142,9 @@ __device__ __forceinline__ unsigned char* lds_base() {
 
 // ---- wave / block primitives (wave64) -----------------------------------------
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (kWave - 1); }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        uint32_t w = __shfl_xor(v, o, kWave);
-        v = w < v ? w : v;
-    }
     return v;
 }
 // Inclusive prefix sum over the wave with DPP row shifts and row broadcasts
@@ -176,6 +158,111 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
     v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false));
     v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));
     return v;
+}
+
+// Reductions over the wave with DPP moves (row_shr 1, 2, 4, 8 inside each
+// 16-lane row, then row_bcast 15 and 31 across rows), the pattern of
+// wave_incl_scan: lane 63 ends with the whole wave's result, which is then
+// broadcast.  A few VALU cycles per step, against a round trip through the LDS
+// crossbar for each step of a shuffle butterfly.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v, uint32_t old) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v), kCtrl, kRowMask, 0xf, false));
+}
+template <class Op>
+__device__ __forceinline__ uint32_t dpp_reduce32(uint32_t v, uint32_t idty, Op op) {
+    v = op(v, dpp_mov<0x111, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x112, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x114, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x118, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x142, 0xa>(v, idty));
+    v = op(v, dpp_mov<0x143, 0xc>(v, idty));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+template <class Op>
+__device__ __forceinline__ uint64_t dpp_reduce64(uint64_t v, uint64_t idty, Op op) {
+    auto step = [&](auto mov) {
+        const uint32_t lo = mov(static_cast<uint32_t>(v), static_cast<uint32_t>(idty));
+        const uint32_t hi = mov(static_cast<uint32_t>(v >> 32), static_cast<uint32_t>(idty >> 32));
+        v = op(v, (static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x111, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x112, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x114, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x118, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x142, 0xa>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x143, 0xc>(x, o); });
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
+    return dpp_reduce32(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    return __uint_as_float(dpp_reduce32(__float_as_uint(v), __float_as_uint(-INFINITY), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
+}
+__device__ __forceinline__ uint64_t wave_min_u64_dpp(uint64_t v) {
+    return dpp_reduce64(v, ~0ull, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+    return dpp_reduce64(v, 0ull, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+}
+// Reductions over the first 16 lanes (one DPP row): row_shr 1, 2, 4, 8, then
+// lane 15 holds the result.  Used to combine per-wave partials that lanes
+// 0..15 have read from LDS in one round trip.
+template <class Op>
+__device__ __forceinline__ uint32_t dpp_reduce16(uint32_t v, uint32_t idty, Op op) {
+    v = op(v, dpp_mov<0x111, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x112, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x114, 0xf>(v, idty));
+    v = op(v, dpp_mov<0x118, 0xf>(v, idty));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 15));
+}
+template <class Op>
+__device__ __forceinline__ uint64_t dpp_reduce16_64(uint64_t v, uint64_t idty, Op op) {
+    auto step = [&](auto mov) {
+        const uint32_t lo = mov(static_cast<uint32_t>(v), static_cast<uint32_t>(idty));
+        const uint32_t hi = mov(static_cast<uint32_t>(v >> 32), static_cast<uint32_t>(idty >> 32));
+        v = op(v, (static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x111, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x112, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x114, 0xf>(x, o); });
+    step([](uint32_t x, uint32_t o) { return dpp_mov<0x118, 0xf>(x, o); });
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 15));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 15));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t row_sum16(uint32_t v) {
+    return dpp_reduce16(v, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+__device__ __forceinline__ uint32_t row_min16(uint32_t v) {
+    return dpp_reduce16(v, ~0u, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint32_t row_max16(uint32_t v) {
+    return dpp_reduce16(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint64_t row_min16_u64(uint64_t v) {
+    return dpp_reduce16_64(v, ~0ull, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint64_t row_max16_u64(uint64_t v) {
+    return dpp_reduce16_64(v, 0ull, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ float wave_max(float v) { return wave_max_dpp(v); }
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) { return wave_sum_dpp(v); }
+__device__ __forceinline__ uint32_t wave_min(uint32_t v) {
+    return dpp_reduce32(v, ~0u, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+    return __longlong_as_double(static_cast<long long>(dpp_reduce64(
+        static_cast<uint64_t>(__double_as_longlong(v)), 0ull, [](uint64_t a, uint64_t b) {
+            return static_cast<uint64_t>(__double_as_longlong(__longlong_as_double(static_cast<long long>(a)) +
+                                                              __longlong_as_double(static_cast<long long>(b))));
+        })));
 }
 
 // Value of `v` in lane `lane` (uniform), as a scalar broadcast.
@@ -232,16 +319,13 @@ template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* tmp, uint32_t* total) {
     constexpr int NW = NT / kWave;
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    static_assert(NW <= 16, "one DPP row combines the waves");
     uint32_t inc = wave_incl_scan(v);
     if (lane == kWave - 1) tmp[wid] = inc;
     TSM_LDS_SYNC();
-    uint32_t before = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) {
-        uint32_t t = tmp[w];
-        before += (w < wid) ? t : 0u;
-        all += t;
-    }
+    // lanes 0..NW-1 read the waves' totals in one round trip
+    const uint32_t t = lane < NW ? tmp[lane] : 0u;
+    const uint32_t before = row_sum16(lane < wid ? t : 0u), all = row_sum16(t);
     TSM_LDS_SYNC();
     *total = all;
     return before + inc - v;
@@ -250,12 +334,11 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* tmp, u
 template <int NT>
 __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* tmp) {
     constexpr int NW = NT / kWave;
+    static_assert(NW <= 16, "one DPP row combines the waves");
     v = wave_sum(v);
     if ((threadIdx.x & (kWave - 1)) == 0) tmp[threadIdx.x / kWave] = v;
     TSM_LDS_SYNC();
-    uint32_t all = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) all += tmp[w];
+    const uint32_t all = row_sum16(lane_id() < NW ? tmp[lane_id()] : 0u);
     TSM_LDS_SYNC();
     return all;
 }
@@ -263,12 +346,11 @@ __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* tmp) {
 template <int NT>
 __device__ __forceinline__ uint32_t block_min(uint32_t v, uint32_t* tmp) {
     constexpr int NW = NT / kWave;
+    static_assert(NW <= 16, "one DPP row combines the waves");
     v = wave_min(v);
     if ((threadIdx.x & (kWave - 1)) == 0) tmp[threadIdx.x / kWave] = v;
     TSM_LDS_SYNC();
-    uint32_t all = 0xFFFFFFFFu;
-#pragma unroll
-    for (int w = 0; w < NW; w++) all = tmp[w] < all ? tmp[w] : all;
+    const uint32_t all = row_min16(lane_id() < NW ? tmp[lane_id()] : 0xFFFFFFFFu);
     TSM_LDS_SYNC();
     return all;
 }

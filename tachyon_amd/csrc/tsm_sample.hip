@@ -91,10 +91,16 @@ __device__ __forceinline__ float thr_float(uint32_t k) { return key_to_float(k);
 __device__ __forceinline__ uint32_t hash_slot(uint32_t id) { return (id * 2654435761u) >> 20; }  // 12 bits
 static_assert(kHashSlots == 4096, "hash_slot yields 12 bits");
 
+// The row's history ids this thread adds to the lookup (ids tid and
+// tid + kBlock of the row's history; ~0 past its end), loaded at the start
+// of the kernel so their latency overlaps the first tiles'.
+constexpr uint32_t kHistPerThread = kHistFast / kBlock;
+static_assert(kHistPerThread * kBlock == kHistFast, "history ids per thread");
+
 // Builds the bitmap of the row's history ids (< n) and their counts.  Needs
 // hlen <= kHistFast (the table then stays at most half full) and n <=
 // 32 * kBitmapWords.  Starts and ends with a barrier.
-__device__ void history_build(const uint32_t* hist, uint32_t hlen, uint32_t n) {
+__device__ __forceinline__ void history_build(const uint32_t (&hid)[kHistPerThread], uint32_t n) {
     const uint32_t tid = threadIdx.x;
     uint32_t* bm = lds_bitmap();
     uint32_t* hk = lds_hkey();
@@ -107,9 +113,10 @@ __device__ void history_build(const uint32_t* hist, uint32_t hlen, uint32_t n) {
         hc[i] = 0;
     }
     TSM_LDS_SYNC();
-    for (uint32_t h = tid; h < hlen; h += kBlock) {
-        const uint32_t id = hist[h];
-        if (id >= n) continue;  // ids past the vocabulary cap are ignored (sampler.rs:171)
+#pragma unroll
+    for (uint32_t k = 0; k < kHistPerThread; k++) {
+        const uint32_t id = hid[k];
+        if (id >= n) continue;  // past the history, or past the vocabulary cap (sampler.rs:171)
         atomicOr(&bm[id >> 5], 1u << (id & 31u));
         uint32_t s = hash_slot(id);
         for (uint32_t probe = 0; probe < kHashSlots; probe++) {
@@ -160,16 +167,13 @@ __device__ __forceinline__ void block_excl_scan3(const uint32_t v[3], uint32_t b
         if (lane == kWave - 1) tmp[g * NW + wid] = inc[g];
     }
     TSM_LDS_SYNC();
+    uint32_t t[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) t[g] = lane < NW ? tmp[g * NW + lane] : 0u;  // one round trip
 #pragma unroll
     for (int g = 0; g < 3; g++) {
-        uint32_t b = 0, all = 0;
-        for (int w = 0; w < NW; w++) {
-            const uint32_t t = tmp[g * NW + w];
-            b += (w < static_cast<int>(wid)) ? t : 0u;
-            all += t;
-        }
-        before[g] = b + inc[g] - v[g];
-        total[g] = all;
+        before[g] = row_sum16(lane < wid ? t[g] : 0u) + inc[g] - v[g];
+        total[g] = row_sum16(t[g]);
     }
     TSM_LDS_SYNC();
 }
@@ -213,28 +217,24 @@ __device__ __forceinline__ void block_minmax3(unsigned long long mn[3], unsigned
     const uint32_t lane = lane_id(), wid = threadIdx.x / kWave;
 #pragma unroll
     for (int g = 0; g < 3; g++) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const unsigned long long a = __shfl_xor(mn[g], o, kWave), b = __shfl_xor(mx[g], o, kWave);
-            mn[g] = a < mn[g] ? a : mn[g];
-            mx[g] = b > mx[g] ? b : mx[g];
-        }
+        mn[g] = wave_min_u64_dpp(mn[g]);
+        mx[g] = wave_max_u64_dpp(mx[g]);
         if (lane == 0) {
             t[(2 * g) * NW + wid] = mn[g];
             t[(2 * g + 1) * NW + wid] = mx[g];
         }
     }
     TSM_LDS_SYNC();
+    unsigned long long a[3], b[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) {  // lanes 0..NW-1 read the waves' values in one round trip
+        a[g] = lane < NW ? t[(2 * g) * NW + lane] : ~0ull;
+        b[g] = lane < NW ? t[(2 * g + 1) * NW + lane] : 0ull;
+    }
 #pragma unroll
     for (int g = 0; g < 3; g++) {
-        unsigned long long a = ~0ull, b = 0;
-        for (int w = 0; w < NW; w++) {
-            const unsigned long long x = t[(2 * g) * NW + w], y = t[(2 * g + 1) * NW + w];
-            a = x < a ? x : a;
-            b = y > b ? y : b;
-        }
-        mn[g] = a;
-        mx[g] = b;
+        mn[g] = row_min16_u64(a[g]);
+        mx[g] = row_max16_u64(b[g]);
     }
     TSM_LDS_SYNC();
 }
@@ -276,7 +276,7 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
         if (with_pen && tg.need[SK_RAW]) {
             for (uint32_t i = tid; i < penn; i += kBlock) {
                 const uint2 e = pen[i];
-                const unsigned long long c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                const unsigned long long c = composite(canon_key(__uint_as_float(e.x)), e.y & kEntId);
                 mn[SK_RAW] = c < mn[SK_RAW] ? c : mn[SK_RAW];
                 mx[SK_RAW] = c > mx[SK_RAW] ? c : mx[SK_RAW];
             }
@@ -318,7 +318,7 @@ __device__ __forceinline__ Sel3 buf_select(uint32_t bufn, uint32_t penn, bool wi
             const int t1 = top[SK_RAW], l1 = lo[SK_RAW];
             for (uint32_t i = tid; i < penn; i += kBlock) {
                 const uint2 e = pen[i];
-                const unsigned long long c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                const unsigned long long c = composite(canon_key(__uint_as_float(e.x)), e.y & kEntId);
                 if (t1 < 64 && (c >> t1) != (known[SK_RAW] >> t1)) continue;
                 atomicAdd(&h3[SK_RAW * kBins + static_cast<uint32_t>((c >> l1) & ((1ull << (t1 - l1)) - 1ull))], 1u);
             }
@@ -440,15 +440,19 @@ __device__ __forceinline__ void count_published(const SHist& h, uint32_t seg0, u
         from = atomicMax(&lds_seg_done()[lane], to);
         from = min(from, to);  // a raise that got further: nothing left here
     }
-    const uint2* buf = lds_buf();
-    for (uint32_t w = 0; w < NW; w++) {
-        const uint32_t f = wave_read(from, w), e = wave_read(to, w);
-        const uint32_t base = seg0 + w * seg_cap;
+    // all segments at once: lane l counts entries l / NW, l / NW + 4, ... of
+    // segment l % NW (the ranges reach the other lanes in one permute)
+    static_assert(kWave == 4 * NW, "four lanes per segment");
+    const uint32_t w = lane % NW, sub = lane / NW;
+    const uint32_t f = static_cast<uint32_t>(__shfl(static_cast<int>(from), static_cast<int>(w), kWave));
+    const uint32_t e = static_cast<uint32_t>(__shfl(static_cast<int>(to), static_cast<int>(w), kWave));
+    if (f + sub < e) {
         // every reading lane acquires the fill itself (it is at least e:
-        // fills only grow), so each lane's reads are ordered after the writes
-        if (f < e) (void)lds_load_acquire(&lds_seg_pub()[w]);
-        for (uint32_t i = f + lane; i < e; i += kWave) {
-            const uint2 en = buf[base + i];
+        // fills only grow), so its reads are ordered after the writes
+        (void)lds_load_acquire(&lds_seg_pub()[w]);
+        const uint2* seg = lds_buf() + seg0 + w * seg_cap;
+        for (uint32_t i = f + sub; i < e; i += kWave / NW) {
+            const uint2 en = seg[i];
             if (!(en.y & kEntPen)) count_kept(__uint_as_float(en.x), (en.y & kEntAllowed) != 0u, h);
         }
     }
@@ -557,6 +561,34 @@ __device__ __forceinline__ void load_tile(const float* rowp, const uint32_t* mp,
             mw[j] = mp[min(id, n - 1u) >> 5];
         }
     }
+}
+
+// The logits half of load_tile (the first tiles' logits are requested before
+// anything else is known about the row).
+template <bool kVecLoads>
+__device__ __forceinline__ void load_logits(const float* rowp, uint32_t tb, uint32_t n, float (&v)[kVec][4]) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < kVec; j++) {
+        if (kVecLoads) {
+            const uint32_t id = min(tb + 4u * (j * kBlock + tid), (n - 1u) & ~3u);
+            const float4 f4 = *reinterpret_cast<const float4*>(rowp + id);
+            v[j][0] = f4.x;
+            v[j][1] = f4.y;
+            v[j][2] = f4.z;
+            v[j][3] = f4.w;
+        } else {
+            const uint32_t id = tb + 4u * (j * kBlock + tid);
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[j][q] = (id + q < n) ? rowp[id + q] : -INFINITY;
+        }
+    }
+}
+// The mask-word half of load_tile.
+__device__ __forceinline__ void load_mask(const uint32_t* mp, uint32_t tb, uint32_t n, uint32_t (&mw)[kVec]) {
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < kVec; j++) mw[j] = mp[min(tb + 4u * (j * kBlock + tid), n - 1u) >> 5];
 }
 
 // The row's last tile: ids past the row read -inf (the clamped loads above
@@ -669,7 +701,8 @@ __device__ __forceinline__ TileFlags tile_prep(const float (&v)[kVec][4], const 
                 const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
                 if (pos < kPenCap)
                     lds_pen()[pos] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
-                                                tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3u));
+                                                (tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3u)) |
+                                                    (((al >> e) & 1u) ? kEntAllowed : 0u));
             }
     }
     TileFlags fl;
@@ -777,7 +810,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
             }
             for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
                 const uint2 e = pen[i];
-                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y & kEntId);
                 best = c < best ? c : best;
             }
 #pragma unroll
@@ -814,7 +847,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
     }
 
     // ---------------- finish ----------------
-    const float u = (a.uniforms && !a.distribution) ? a.uniforms[row] : 0.0f;
+    const float u = f.u;
     DistOut dist;
     const DistOut* dptr = nullptr;
     if (a.distribution) {
@@ -923,7 +956,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
             }
             for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
                 const uint2 e = pen[i];
-                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y);
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y & kEntId);
                 if (c <= sel.T[SK_RAW]) {
                     const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
                     if (pos < kExactCap) gcomp[pos] = c;
@@ -948,22 +981,601 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Ta
     }
 }
 
+// ---- single-wave finish ------------------------------------------------------------
+// The common rows (top-k, a valid candidate buffer, a ranked list of at most
+// 64, not distribution mode) are finished by one wave without a block
+// barrier: the block first filters the buffer against the final thresholds
+// into two lists (two barriers), then waves 1-15 leave and wave 0 selects,
+// sorts and applies the reference's arithmetic.  Within the wave, lanes talk
+// through LDS between wave barriers (the wave runs in lockstep; the barrier
+// keeps the compiler from reordering across it).
+constexpr uint32_t kWaveList = 64;                  // longest ranked list the wave finish takes
+constexpr uint32_t kListCap = kBufCap;              // entries of each filtered list
+__device__ __forceinline__ uint2* lds_swin() { return reinterpret_cast<uint2*>(lds_base()); }  // region A
+__device__ __forceinline__ uint64_t* lds_sraw() { return reinterpret_cast<uint64_t*>(lds_base() + kListCap * 8); }
+__device__ __forceinline__ uint32_t* lds_whist() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHist); }
+__device__ __forceinline__ uint64_t* lds_wlist() { return reinterpret_cast<uint64_t*>(lds_base() + kOffHist + 1024); }
+static_assert(kListCap * 16 <= kRegionA, "both filtered lists fit region A");
+static_assert(1024 + kWaveList * 8 <= kBins * 12, "wave scratch fits the histogram region");
+
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long w = __shfl_xor(v, o, kWave);
+        v = w < v ? w : v;
+    }
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned long long w = __shfl_xor(v, o, kWave);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// The k-th smallest (1-based) of the keys key_of(i, &c) gives for i < n
+// (false: not in the set); ~0 when the set has fewer than k keys.  Keys are
+// distinct (an id in the low bits).  Radix rounds of 8 bits over a 256-bin
+// LDS histogram, from the highest bit where the keys differ; bits 22..31 of a
+// composite are zero and skipped; a round whose bin holds one key ends early.
+template <class KeyOf>
+__device__ uint64_t wave_kth(uint32_t n, uint32_t k, KeyOf key_of) {
+    const uint32_t lane = lane_id();
+    uint32_t* hist = lds_whist();
+    unsigned long long mn = ~0ull, mx = 0;
+    uint32_t cnt = 0;
+    for (uint32_t i = lane; i < n; i += kWave) {
+        uint64_t c;
+        if (key_of(i, &c)) {
+            mn = c < mn ? c : mn;
+            mx = c > mx ? c : mx;
+            cnt++;
+        }
+    }
+    mn = wave_min_u64(mn);
+    mx = wave_max_u64(mx);
+    cnt = wave_sum(cnt);
+    if (k == 0 || cnt < k) return ~0ull;
+    if (cnt == 1) return mn;
+    int top = high_bit64(mn ^ mx) + 1;  // bits >= top are common to every key
+    uint64_t prefix = top >= 64 ? 0ull : (mn >> top) << top;
+    uint32_t need = k;
+    while (top > 0) {
+        if (top > 22 && top <= 32) top = 22;  // the zero bits of a composite
+        const int lo = top > 8 ? top - 8 : 0;
+        const uint32_t width_mask = (1u << (top - lo)) - 1u;
+#pragma unroll
+        for (int b = 0; b < 4; b++) hist[lane * 4 + b] = 0;
+        __builtin_amdgcn_wave_barrier();
+        for (uint32_t i = lane; i < n; i += kWave) {
+            uint64_t c;
+            if (key_of(i, &c) && (top >= 64 || (c >> top) == (prefix >> top)))
+                atomicAdd(&hist[static_cast<uint32_t>(c >> lo) & width_mask], 1u);
+        }
+        __builtin_amdgcn_wave_barrier();
+        uint32_t h[4], sum = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            h[b] = hist[lane * 4 + b];
+            sum += h[b];
+        }
+        const uint32_t incl = wave_incl_scan(sum);
+        const uint64_t hit = wave_ballot(incl >= need);
+        const uint32_t L = static_cast<uint32_t>(__builtin_ctzll(hit));  // the set holds >= need keys here
+        uint32_t run = incl - sum, d = 0, before = 0, inbin = 0;
+        bool done = false;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (!done && run + h[b] >= need) {
+                d = lane * 4 + b;
+                before = run;
+                inbin = h[b];
+                done = true;
+            }
+            run += h[b];
+        }
+        d = wave_read(d, L);
+        before = wave_read(before, L);
+        inbin = wave_read(inbin, L);
+        __builtin_amdgcn_wave_barrier();  // every lane has read the bins before the next round clears them
+        prefix |= static_cast<uint64_t>(d) << lo;
+        need -= before;
+        top = lo;
+        if (inbin == 1 && top > 0) {
+            // the only key with this prefix
+            unsigned long long f = ~0ull;
+            for (uint32_t i = lane; i < n; i += kWave) {
+                uint64_t c;
+                if (key_of(i, &c) && (c >> top) == (prefix >> top)) f = c;
+            }
+            return wave_min_u64(f);
+        }
+    }
+    return prefix;
+}
+
+// Register-resident lists for the wave finish: entry i of a list of n sits
+// in slot r = i / 64 of lane i % 64 (kWaveRegs slots per lane).
+constexpr uint32_t kWaveRegs = 16;
+constexpr uint32_t kWaveRegCap = kWaveRegs * kWave;
+
+// wave_kth over a register list: key_of(r, &c) gives the key of this lane's
+// slot r (false: not in the set); slots at or past n are never asked.
+template <class KeyOf>
+__device__ __forceinline__ uint64_t wave_kth_reg(uint32_t n, uint32_t k, KeyOf key_of) {
+    const uint32_t lane = lane_id();
+    uint32_t* hist = lds_whist();
+    unsigned long long mn = ~0ull, mx = 0;
+    uint32_t cnt = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < kWaveRegs; r++) {
+        if (r * kWave >= n) break;
+        uint64_t c;
+        if (r * kWave + lane < n && key_of(r, &c)) {
+            mn = c < mn ? c : mn;
+            mx = c > mx ? c : mx;
+            cnt++;
+        }
+    }
+    mn = wave_min_u64_dpp(mn);
+    mx = wave_max_u64_dpp(mx);
+    cnt = wave_sum_dpp(cnt);
+    if (k == 0 || cnt < k) return ~0ull;
+    if (cnt == 1) return mn;
+    int top = high_bit64(mn ^ mx) + 1;
+    uint64_t prefix = top >= 64 ? 0ull : (mn >> top) << top;
+    uint32_t need = k;
+    while (top > 0) {
+        if (top > 22 && top <= 32) top = 22;  // the zero bits of a composite
+        const int lo = top > 8 ? top - 8 : 0;
+        const uint32_t width_mask = (1u << (top - lo)) - 1u;
+#pragma unroll
+        for (int b = 0; b < 4; b++) hist[lane * 4 + b] = 0;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (uint32_t r = 0; r < kWaveRegs; r++) {
+            if (r * kWave >= n) break;
+            uint64_t c;
+            if (r * kWave + lane < n && key_of(r, &c) && (top >= 64 || (c >> top) == (prefix >> top)))
+                atomicAdd(&hist[static_cast<uint32_t>(c >> lo) & width_mask], 1u);
+        }
+        __builtin_amdgcn_wave_barrier();
+        uint32_t h[4], sum = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            h[b] = hist[lane * 4 + b];
+            sum += h[b];
+        }
+        const uint32_t incl = wave_incl_scan(sum);
+        const uint32_t L = static_cast<uint32_t>(__builtin_ctzll(wave_ballot(incl >= need)));
+        uint32_t run = incl - sum, d = 0, before = 0, inbin = 0;
+        bool done = false;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (!done && run + h[b] >= need) {
+                d = lane * 4 + b;
+                before = run;
+                inbin = h[b];
+                done = true;
+            }
+            run += h[b];
+        }
+        d = wave_read(d, L);
+        before = wave_read(before, L);
+        inbin = wave_read(inbin, L);
+        __builtin_amdgcn_wave_barrier();
+        prefix |= static_cast<uint64_t>(d) << lo;
+        need -= before;
+        top = lo;
+        if (inbin == 1 && top > 0) {
+            unsigned long long f = ~0ull;
+#pragma unroll
+            for (uint32_t r = 0; r < kWaveRegs; r++) {
+                if (r * kWave >= n) break;
+                uint64_t c;
+                if (r * kWave + lane < n && key_of(r, &c) && (c >> top) == (prefix >> top)) f = c;
+            }
+            return wave_min_u64_dpp(f);
+        }
+    }
+    return prefix;
+}
+
+// Writes the register list's keys key_of gives (true) into lds_wlist(), in
+// any order; returns how many.
+template <class KeyOf>
+__device__ __forceinline__ uint32_t wave_gather_reg(uint32_t n, KeyOf key_of) {
+    const uint32_t lane = lane_id();
+    uint64_t* out = lds_wlist();
+    uint32_t cnt = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < kWaveRegs; r++) {
+        if (r * kWave >= n) break;
+        uint64_t c = 0;
+        const bool in = r * kWave + lane < n && key_of(r, &c);
+        const uint64_t b = wave_ballot(in);
+        if (in) out[cnt + lanes_below(b)] = c;
+        cnt += static_cast<uint32_t>(__popcll(b));
+    }
+    __builtin_amdgcn_wave_barrier();
+    return cnt;
+}
+
+// Sorts one u64 per lane ascending across the wave (bitonic; lanes past the
+// list hold ~0).
+__device__ __forceinline__ uint64_t wave_sort64(uint64_t v) {
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (uint32_t k = 2; k <= static_cast<uint32_t>(kWave); k <<= 1)
+#pragma unroll
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            const unsigned long long o = __shfl_xor(static_cast<unsigned long long>(v), static_cast<int>(j), kWave);
+            const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
+            v = keep_min ? (o < v ? o : v) : (o > v ? o : v);
+        }
+    return v;
+}
+
+__device__ __forceinline__ uint64_t* lds_wsort() { return reinterpret_cast<uint64_t*>(lds_base() + kOffHist + 1024 + kWaveList * 8); }
+static_assert(1024 + 2 * kWaveList * 8 <= kBins * 12, "wave sort scratch fits the histogram region");
+
+// Sorts the keys of lanes < n (n <= 64, distinct) ascending: each lane counts
+// the smaller keys from scalar broadcasts of the others', then the keys
+// trade places through LDS.  Lanes >= n get ~0.
+__device__ __forceinline__ uint64_t wave_sort_rank(uint64_t v, uint32_t n) {
+    const uint32_t lane = lane_id();
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < n; j++) {
+        const uint64_t o = (static_cast<uint64_t>(wave_read(static_cast<uint32_t>(v >> 32), j)) << 32) |
+                           wave_read(static_cast<uint32_t>(v), j);
+        rank += o < v ? 1u : 0u;
+    }
+    uint64_t* t = lds_wsort();
+    if (lane < n) t[rank] = v;
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t r = lane < n ? t[lane] : ~0ull;
+    __builtin_amdgcn_wave_barrier();
+    return r;
+}
+
+// The reference's arithmetic on a ranked list held one entry per lane (lane
+// j: value y, best first, j < len <= 64), as exact_finalize does it:
+// p_j = expf((y_j - y_0) / t) (sampler.rs:231-234), min-p, top-p
+// (sampler.rs:235-246) and the draw (sampler.rs:142-150), every fold in list
+// order so the roundings are the CPU sampler's.
+__device__ __forceinline__ Pick wave_finalize(float y, uint32_t id, uint32_t len, float u, const RowMode& m,
+                                              const tsm_row_params& P) {
+    const uint32_t lane = lane_id();
+    const float y0 = readlane_f(y, 0);
+    const float p = lane < len ? glibc_expf((y - y0) / m.t) : 0.0f;
+    if (!m.greedy && P.min_p > 0.0f) {
+        const uint64_t below = wave_ballot(lane < len && !(p >= P.min_p));
+        if (below) len = max(static_cast<uint32_t>(__builtin_ctzll(below)), 1u);
+    }
+    // prefix sums (left fold) of p over the list
+    float total = 0.0f, pre = 0.0f;
+    for (uint32_t j = 0; j < len; j++) {
+        total += readlane_f(p, j);
+        pre = lane == j ? total : pre;
+    }
+    uint32_t keep = len;
+    if (!(m.greedy || P.top_p >= 1.0f)) {
+        const float q = lane < len ? p / total : 0.0f;
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < len; j++) {
+            acc += readlane_f(q, j);
+            if (acc >= P.top_p) {
+                keep = j + 1;
+                break;
+            }
+        }
+    }
+    const float mass = readlane_f(pre, keep - 1);
+    uint32_t pick = keep - 1;
+    float r = u * mass;
+    for (uint32_t j = 0; j < keep; j++) {
+        r -= readlane_f(p, j);
+        if (r <= 0.0f) {
+            pick = j;
+            break;
+        }
+    }
+    Pick out;
+    out.token = wave_read(id, pick);
+    out.keep = keep;
+    out.prob = readlane_f(p, pick) / mass;
+    out.mass = mass;
+    return out;
+}
+
+// Writes into lds_wlist() the keys key_of gives (true) for i < n, in any
+// order; returns how many.
+template <class KeyOf>
+__device__ __forceinline__ uint32_t wave_gather(uint32_t n, KeyOf key_of) {
+    const uint32_t lane = lane_id();
+    uint64_t* out = lds_wlist();
+    uint32_t cnt = 0;
+    for (uint32_t i0 = 0; i0 < n; i0 += kWave) {
+        const uint32_t i = i0 + lane;
+        uint64_t c = 0;
+        const bool in = i < n && key_of(i, &c);
+        const uint64_t b = wave_ballot(in);
+        if (in) out[cnt + lanes_below(b)] = c;
+        cnt += static_cast<uint32_t>(__popcll(b));
+    }
+    __builtin_amdgcn_wave_barrier();
+    return cnt;
+}
+
+// The finish of a row by one wave (see above).  The whole block takes part
+// in the filtering; returns false, before any wave leaves, when a list does
+// not fit (the caller then runs the block finish), true once the row is done.
+// Inlined: were the kernel's argument block passed by reference to a function
+// that is not inlined, it would escape, every pointer read from it would lose
+// its global address space, and the stream's loads would become flat loads
+// (which every LDS wait then also waits for).
+__device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, const Targets tg0, const uint32_t nlp, const float lref,
+                            const double lsum, const uint32_t nallow, const uint32_t bufn) {
+    constexpr uint32_t NW = kBlock / kWave;
+    constexpr uint32_t kB = kBufCap / NW / kWave;  // buffer entries per lane in a wave's slice
+    constexpr uint32_t kP = kPenCap / NW / kWave;  // penalized-list entries per lane
+    const uint32_t row = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wid = tid / kWave;
+    const RowMode m = f.m;
+    uint32_t* misc = lds_misc();
+    uint32_t* tmp = lds_tmp();
+    double* md = lds_miscd();
+    unsigned long long* mbest = reinterpret_cast<unsigned long long*>(md + NW);
+    const uint2* buf = lds_buf();
+    const uint2* pen = lds_pen();
+    const float tA = thr_float(misc[M_THR + static_cast<uint32_t>(SK_ALL)]);
+    const float tR = thr_float(misc[M_THR + static_cast<uint32_t>(SK_RAW)]);
+    const float tL = thr_float(misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)]);
+    const uint32_t penn = min(misc[M_PENN], kPenCap);
+    const bool need_raw = tg0.need[SK_RAW] > 0;
+
+    // ---- the block: each wave filters its slice of the buffer (window and
+    // fallback candidates at or above the final thresholds; raw candidates)
+    // and of the penalized list (raw candidates, by raw value) ----
+    const uint32_t bseg = (bufn + NW - 1) / NW, pseg = (penn + NW - 1) / NW;
+    uint2 we[kB];
+    bool win[kB], rawk[kB], prk[kP];
+    uint64_t pc[kP];
+    unsigned long long best = ~0ull;  // the best raw (value desc, id asc)
+    uint32_t cw = 0, cr = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kB; k++) {
+        const uint32_t j = lane + k * kWave, i = wid * bseg + j;
+        win[k] = rawk[k] = false;
+        we[k] = make_uint2(0u, 0u);
+        if (j < bseg && i < bufn) {
+            const uint2 e = buf[i];
+            const float y = __uint_as_float(e.x);
+            win[k] = keep2(y, (e.y & kEntAllowed) != 0u, tA, tL);
+            if (!(e.y & kEntPen)) {
+                const unsigned long long c = composite(canon_key(y), e.y & kEntId);
+                best = c < best ? c : best;
+                rawk[k] = need_raw && y >= tR;
+            }
+            we[k] = e;
+        }
+        cw += static_cast<uint32_t>(__popcll(wave_ballot(win[k])));
+        cr += static_cast<uint32_t>(__popcll(wave_ballot(rawk[k])));
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kP; k++) {
+        const uint32_t j = lane + k * kWave, i = wid * pseg + j;
+        prk[k] = false;
+        pc[k] = 0;
+        if (j < pseg && i < penn) {
+            const uint2 e = pen[i];
+            const float x = __uint_as_float(e.x);
+            const unsigned long long c = composite(canon_key(x), e.y & kEntId);
+            best = c < best ? c : best;
+            prk[k] = need_raw && x >= tR;
+            pc[k] = c;
+        }
+        cr += static_cast<uint32_t>(__popcll(wave_ballot(prk[k])));
+    }
+    // the wave's shares of the allowed count and of the logsumexp (its own
+    // reference: the largest of its threads')
+    const uint32_t nallow_w = wave_sum_dpp(nallow);
+    const float mref = wave_max_dpp(lsum > 0.0 ? lref : -INFINITY);
+    double sw = lsum > 0.0 ? lsum * exp(static_cast<double>(lref) - static_cast<double>(mref)) : 0.0;
+    sw = wave_sum_f64_dpp(sw);
+    best = wave_min_u64_dpp(best);
+    if (lane == 0) {
+        tmp[wid] = cw;
+        tmp[NW + wid] = cr;
+        tmp[2 * NW + wid] = nallow_w;
+        tmp[3 * NW + wid] = __float_as_uint(mref);
+        md[wid] = sw;
+        mbest[wid] = best;
+    }
+    TSM_LDS_SYNC();
+    const uint32_t c1 = lane < NW ? tmp[lane] : 0u, c2 = lane < NW ? tmp[NW + lane] : 0u;  // one round trip
+    uint32_t bw = row_sum16(lane < wid ? c1 : 0u), br = row_sum16(lane < wid ? c2 : 0u);
+    const uint32_t nwin = row_sum16(c1), nraw_all = row_sum16(c2);
+    const bool fits = nwin <= kWaveRegCap && nraw_all <= kWaveRegCap;  // wave 0 holds both in registers
+    if (fits) {
+        uint2* swin = lds_swin();
+        uint64_t* sraw = lds_sraw();
+#pragma unroll
+        for (uint32_t k = 0; k < kB; k++) {
+            const uint64_t b = wave_ballot(win[k]);
+            if (win[k]) swin[bw + lanes_below(b)] = we[k];
+            bw += static_cast<uint32_t>(__popcll(b));
+            const uint64_t b2 = wave_ballot(rawk[k]);
+            if (rawk[k]) sraw[br + lanes_below(b2)] = composite(canon_key(__uint_as_float(we[k].x)), we[k].y & kEntId);
+            br += static_cast<uint32_t>(__popcll(b2));
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kP; k++) {
+            const uint64_t b = wave_ballot(prk[k]);
+            if (prk[k]) sraw[br + lanes_below(b)] = pc[k];
+            br += static_cast<uint32_t>(__popcll(b));
+        }
+    }
+    TSM_LDS_SYNC();
+    if (!fits) return false;
+    if (wid != 0) return true;
+
+    // ---- wave 0 ----
+    const uint32_t nallow_all = wave_sum_dpp(lane < NW ? tmp[2 * NW + lane] : 0u);
+    const unsigned long long raw_best = wave_min_u64_dpp(lane < NW ? mbest[lane] : ~0ull);
+    float lse = 0.0f;
+    if (m.logprobs) {
+        // sampler.rs:298-304: lse = max + (f32) ln(sum exp((f64)(l - max)))
+        const float rmax = key_to_float(~static_cast<uint32_t>(raw_best >> 32));
+        double term = 0.0;
+        if (lane < NW) {
+            const float mw = __uint_as_float(tmp[3 * NW + lane]);
+            if (mw != -INFINITY) term = md[lane] * exp(static_cast<double>(mw) - static_cast<double>(rmax));
+        }
+        lse = rmax + static_cast<float>(log(wave_sum_f64_dpp(term)));
+    }
+    const float u = f.u;
+    Pick pk;
+    pk.token = 0;
+    pk.keep = 0;
+    pk.prob = 1.0f;
+    pk.mass = 0.0f;
+    if (m.constrained && nallow_all == 0) {
+        pk.token = static_cast<uint32_t>(raw_best);  // nothing allowed: the raw argmax (sampler.rs:139-141)
+    } else {
+        // the window list, in registers
+        uint2 wl[kWaveRegs];
+        {
+            const uint2* swin = lds_swin();
+#pragma unroll
+            for (uint32_t r = 0; r < kWaveRegs; r++) {
+                const uint32_t i = r * kWave + lane;
+                wl[r] = i < nwin ? swin[i] : make_uint2(0u, 0u);
+            }
+        }
+        auto canon_all = [&](uint32_t r, uint64_t* c) {
+            *c = composite(canon_key(__uint_as_float(wl[r].x)), wl[r].y & kEntId);
+            return true;
+        };
+        // the window boundary: the W-th best by IEEE order (top_n, sampler.rs:192-194)
+        const uint64_t tw = wave_kth_reg(nwin, m.window, canon_all);
+        uint32_t g;
+        if (!m.constrained) {
+            g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return canon_all(r, c) && *c <= tw; });
+        } else {
+            // allowed ids inside the window (sampler.rs:209-210)
+            auto in_window = [&](uint32_t r, uint64_t* c) {
+                if (!(wl[r].y & kEntAllowed)) return false;
+                return canon_all(r, c) && *c <= tw;
+            };
+            uint32_t inw = 0;
+#pragma unroll
+            for (uint32_t r = 0; r < kWaveRegs; r++) {
+                if (r * kWave >= nwin) break;
+                uint64_t c;
+                inw += (r * kWave + lane < nwin && in_window(r, &c)) ? 1u : 0u;
+            }
+            inw = wave_sum_dpp(inw);
+            if (inw > 0) {
+                const uint64_t ta = inw > m.want ? wave_kth_reg(nwin, m.want, in_window) : ~0ull;
+                g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return in_window(r, c) && *c <= ta; });
+            } else {
+                // none in the window: the best allowed ids of the whole row by
+                // f32::total_cmp (sampler.rs:211-221)
+                auto allowed_total = [&](uint32_t r, uint64_t* c) {
+                    if (!(wl[r].y & kEntAllowed)) return false;
+                    *c = composite(total_key(__uint_as_float(wl[r].x)), wl[r].y & kEntId);
+                    return true;
+                };
+                const uint64_t tf = wave_kth_reg(nwin, m.want, allowed_total);
+                g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return allowed_total(r, c) && *c <= tf; });
+            }
+        }
+        const uint32_t len = min(g, m.want);
+        const uint64_t mine = wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
+        if (len == 0) {
+            pk.token = 0xFFFFFFFFu;  // nothing to rank (e.g. NaN logits): flagged below
+        } else {
+            const float y = key_to_float(~static_cast<uint32_t>(mine >> 32));
+            pk = wave_finalize(y, static_cast<uint32_t>(mine), len, u, m, f.P);
+        }
+    }
+
+    // ---- outputs ----
+    if (pk.token >= f.n) {
+        if (lane == 0) atomicOr(a.status, TSM_STATUS_INTERNAL);
+        pk.token = 0;
+    }
+    // the token's raw logit is requested now and used last, after the raw top-n
+    const float x_tok = (m.logprobs && a.out_logprob) ? f.rowp[pk.token] : 0.0f;
+    if (nlp > 0) {
+        // raw top-n (sampler.rs:305-311), ties -> lower id
+        uint64_t rl[kWaveRegs];
+        {
+            const uint64_t* sraw = lds_sraw();
+#pragma unroll
+            for (uint32_t r = 0; r < kWaveRegs; r++) {
+                const uint32_t i = r * kWave + lane;
+                rl[r] = i < nraw_all ? sraw[i] : ~0ull;
+            }
+        }
+        auto raw_key = [&](uint32_t r, uint64_t* c) {
+            *c = rl[r];
+            return true;
+        };
+        const uint64_t tr = wave_kth_reg(nraw_all, nlp, raw_key);
+        const uint32_t g = wave_gather_reg(nraw_all, [&](uint32_t r, uint64_t* c) { return raw_key(r, c) && *c <= tr; });
+        const uint64_t mine = wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
+        const uint32_t nraw = min(g, nlp);
+        if (lane < nraw) {
+            const size_t o = static_cast<size_t>(row) * a.top_stride + lane;
+            a.out_top_ids[o] = static_cast<uint32_t>(mine);
+            if (a.out_top_lp) a.out_top_lp[o] = key_to_float(~static_cast<uint32_t>(mine >> 32)) - lse;
+        }
+    }
+    if (lane == 0) {
+        a.out_token[row] = pk.token;
+        if (a.out_prob) a.out_prob[row] = pk.prob;
+        if (a.out_keep) a.out_keep[row] = pk.keep;
+        if (m.logprobs && a.out_logprob) a.out_logprob[row] = x_tok - lse;
+    }
+    return true;
+}
+
 template <bool kVecLoads>
 __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const uint32_t n = a.usable;
-    const tsm_row_params P = a.params[row];
+    // first the loads nothing waits for: the first two tiles' logits, the row's
+    // history offsets and parameters and its uniform, then its history ids
+    // (every later load waits on one of these; requested together, their
+    // latencies overlap)
+    float v[kVec][4], vB[kVec][4], vC[kVec][4];
+    uint32_t mw[kVec], mwB[kVec], mwC[kVec];
+    const float* rowp0 = a.logits + static_cast<size_t>(row) * a.row_stride;
+    load_logits<kVecLoads>(rowp0, 0, n, v);
+    load_logits<kVecLoads>(rowp0, kTile, n, vB);
     uint32_t h0 = 0, hlen = 0;
     if (a.hist_off) {
         h0 = a.hist_off[row];
         const uint32_t h1 = a.hist_off[row + 1];
         hlen = h1 > h0 ? h1 - h0 : 0u;
     }
+    const tsm_row_params P = a.params[row];
+    const float u_row = (a.uniforms && !a.distribution) ? a.uniforms[row] : 0.0f;
+    uint32_t hid[kHistPerThread];
+#pragma unroll
+    for (uint32_t k = 0; k < kHistPerThread; k++) {
+        const uint32_t h = tid + k * kBlock;
+        hid[k] = (a.hist_ids && h < hlen && hlen <= kHistFast) ? a.hist_ids[h0 + h] : 0xFFFFFFFFu;
+    }
     Fin f;
-    f.rowp = a.logits + static_cast<size_t>(row) * a.row_stride;
+    f.rowp = rowp0;
     f.hist = a.hist_ids ? a.hist_ids + h0 : nullptr;
     f.hlen = hlen;
     f.n = n;
+    f.u = u_row;
     // distribution() takes no constraint (sampler.rs:102-116)
     f.m = row_mode(P, n, hlen, a.mask != nullptr && !a.distribution);
     f.mrow = f.m.constrained ? a.mask + static_cast<size_t>(row) * a.mask_stride : nullptr;
@@ -1005,16 +1617,14 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     }
     // three register sets take the tiles in turn (tile t in set t mod 3):
     // tiles t+1 and t+2 are in flight while tile t is processed, and no set is
-    // ever copied to another (a copy would wait for its loads)
-    float v[kVec][4], vB[kVec][4], vC[kVec][4];
-    uint32_t mw[kVec], mwB[kVec], mwC[kVec];
-    // the mask words are read unconditionally, from the logits when there is no mask
-    const uint32_t* mp = mrow ? mrow : reinterpret_cast<const uint32_t*>(rowp);
+    // ever copied to another (a copy would wait for its loads).  The mask
+    // words are read unconditionally, from the logits when there is no mask
     // (loads past the row's last tile read in bounds and go unused: an
-    // unconditional load keeps one code path)
-    load_tile<kVecLoads>(rowp, mp, 0, n, v, mw);  // in flight while the lookup is built
-    load_tile<kVecLoads>(rowp, mp, kTile, n, vB, mwB);
-    if (pen_lookup) history_build(f.hist, hlen, n);  // barriers inside
+    // unconditional load keeps one code path).
+    const uint32_t* mp = mrow ? mrow : reinterpret_cast<const uint32_t*>(rowp);
+    load_mask(mp, 0, n, mw);
+    load_mask(mp, kTile, n, mwB);
+    if (pen_lookup) history_build(hid, n);  // barriers inside
 
     SHist sh;
     sh.base[0] = sh.base[1] = kKeyUntracked;
@@ -1229,12 +1839,8 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         }
         if (lane == 0) lds_tmp()[wid] = kept_w;
         TSM_LDS_SYNC();
-        uint32_t before = 0, fill0 = seg0;
-        for (uint32_t w = 0; w < kBlock / kWave; w++) {
-            const uint32_t c = lds_tmp()[w];
-            before += w < wid ? c : 0u;
-            fill0 += c;
-        }
+        const uint32_t cw = lane < kBlock / kWave ? lds_tmp()[lane] : 0u;  // one round trip
+        const uint32_t before = row_sum16(lane < wid ? cw : 0u), fill0 = seg0 + row_sum16(cw);
         uint32_t dst = seg0 + before;
 #pragma unroll
         for (uint32_t k = 0; k < kSegRegs; k++) {
@@ -1251,9 +1857,9 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             const uint32_t penn = min(penn0, kPenCap);
             for (uint32_t i = tid; i < penn; i += kBlock) {
                 const uint2 e = pen[i];
-                const uint32_t id = e.y;
+                const uint32_t id = e.y & kEntId;
                 const float y = penalize(__uint_as_float(e.x), history_count(id), m, P);
-                const bool al = m.constrained && ((mrow[id >> 5] >> (id & 31u)) & 1u);
+                const bool al = (e.y & kEntAllowed) != 0u;
                 if (keep2(y, al, tA, tL)) {
                     const uint32_t pos = atomicAdd(&misc[M_BUFN], 1u);
                     if (pos < kBufCap) buf[pos] = make_uint2(__float_as_uint(y), id | kEntPen | (al ? kEntAllowed : 0u));
@@ -1264,6 +1870,13 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         const uint32_t fill = misc[M_BUFN];
         if (tid == 0 && (fill > kBufCap || misc[M_OVF] != 0u)) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
         bufn = min(fill, kBufCap);
+    }
+    // the finish: one wave for the common rows, the whole block otherwise
+    TSM_LDS_SYNC();
+    const uint32_t flags = misc[M_FLAGS];
+    if (tracking && !(flags & (ROWF_BUF_OVERFLOW | ROWF_SLOW_HISTORY)) && m.topk && !a.distribution &&
+        m.want <= kWaveList && nlp <= kWaveList) {
+        if (finish_wave(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn)) return;
     }
     finish_row(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn);
 }

@@ -91,6 +91,7 @@ struct Fin {
     const uint32_t* mrow;
     const uint32_t* hist;
     uint32_t hlen, n;
+    float u;  // the row's uniform draw (0 for distribution())
     RowMode m;
     tsm_row_params P;
     __device__ __forceinline__ uint32_t* cnt() const { return reinterpret_cast<uint32_t*>(lds_base() + kOffCnt); }
