@@ -140,6 +140,18 @@ __device__ __forceinline__ unsigned char* lds_base() {
     return tsm_lds;
 }
 
+// Memory the kernel only reads, at addresses uniform over the workgroup (the
+// row's parameters, history offsets and uniform): loads through the constant
+// address space become scalar loads, which count on their own counter, so
+// waiting for them does not wait for the vector loads already in flight.
+#ifndef TSM_CONST_AS
+#define TSM_CONST_AS __attribute__((address_space(4)))
+#endif
+template <class T>
+__device__ __forceinline__ const TSM_CONST_AS T* const_as(const T* p) {
+    return (const TSM_CONST_AS T*)p;
+}
+
 // ---- wave / block primitives (wave64) -----------------------------------------
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ double wave_sum(double v) {
@@ -256,6 +268,9 @@ __device__ __forceinline__ float wave_max(float v) { return wave_max_dpp(v); }
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v) { return wave_sum_dpp(v); }
 __device__ __forceinline__ uint32_t wave_min(uint32_t v) {
     return dpp_reduce32(v, ~0u, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    return dpp_reduce32(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
 }
 __device__ __forceinline__ double wave_sum_f64_dpp(double v) {
     return __longlong_as_double(static_cast<long long>(dpp_reduce64(

@@ -95,6 +95,11 @@ static_assert(kHashSlots == 4096, "hash_slot yields 12 bits");
 // tid + kBlock of the row's history; ~0 past its end), loaded at the start
 // of the kernel so their latency overlaps the first tiles'.
 constexpr uint32_t kHistPerThread = kHistFast / kBlock;
+
+// Words read in place of an absent optional input (history offsets, uniforms),
+// so that the loads at the start of the kernel need no branch: a branch
+// would end the block there and force a wait on every load issued so far.
+__device__ uint32_t kZeroWords[4];
 static_assert(kHistPerThread * kBlock == kHistFast, "history ids per thread");
 
 // Builds the bitmap of the row's history ids (< n) and their counts.  Needs
@@ -593,6 +598,20 @@ __device__ __forceinline__ void load_mask(const uint32_t* mp, uint32_t tb, uint3
 
 // The row's last tile: ids past the row read -inf (the clamped loads above
 // hold other ids' values there).
+// Marks a tile's registers as used here, on every path.  A loaded register
+// that some path never reads (the mask words of an unconstrained row, the
+// logits of a row that tracks nothing) stays a pending load in the
+// compiler's wait analysis until it is overwritten; the loop then waits for
+// it where the next prefetch reuses the register, which drains the prefetch
+// pipeline.  Taking them here puts that wait where the tile is consumed
+// anyway.
+__device__ __forceinline__ void tile_arrived(const float (&v)[kVec][4], const uint32_t (&mw)[kVec]) {
+#pragma unroll
+    for (int j = 0; j < kVec; j++) {
+        asm volatile("" ::"v"(v[j][0]), "v"(v[j][1]), "v"(v[j][2]), "v"(v[j][3]), "v"(mw[j]));
+    }
+}
+
 __device__ __forceinline__ void mask_tail(float (&v)[kVec][4], uint32_t tb, uint32_t n) {
     if (tb + kTile <= n) return;  // uniform
     const uint32_t tid = threadIdx.x;
@@ -767,8 +786,12 @@ __device__ __forceinline__ void stream_write(const float (&v)[kVec][4], const Ti
 
 // After the streaming pass: logsumexp and allowed count, then the pick (or
 // the distribution) and the logprobs of the row.
-__device__ __forceinline__ void finish_row(const SampleArgs& a, Fin& f, const Targets tg0, const uint32_t nlp,
-                                           const float lref, const double lsum, uint32_t nallow, uint32_t bufn) {
+__device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in, const Targets tg0,
+                                           const uint32_t nlp, const float lref, const double lsum, uint32_t nallow,
+                                           uint32_t bufn) {
+    // the re-read functions take the row by reference, which puts it in
+    // scratch memory: the copy made here keeps those stores on this path
+    Fin f = f_in;
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const uint32_t n = f.n;
     const RowMode m = f.m;
@@ -1227,10 +1250,16 @@ static_assert(1024 + 2 * kWaveList * 8 <= kBins * 12, "wave sort scratch fits th
 __device__ __forceinline__ uint64_t wave_sort_rank(uint64_t v, uint32_t n) {
     const uint32_t lane = lane_id();
     uint32_t rank = 0;
-    for (uint32_t j = 0; j < n; j++) {
-        const uint64_t o = (static_cast<uint64_t>(wave_read(static_cast<uint32_t>(v >> 32), j)) << 32) |
-                           wave_read(static_cast<uint32_t>(v), j);
-        rank += o < v ? 1u : 0u;
+    // eight lanes per step with constant lane indices (no loop-carried
+    // scalar index, no branch per lane); a key past the list (~0) is never
+    // below a listed one
+    for (uint32_t j0 = 0; j0 < n; j0 += 8) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint64_t o = (static_cast<uint64_t>(wave_read(static_cast<uint32_t>(v >> 32), j0 + i)) << 32) |
+                               wave_read(static_cast<uint32_t>(v), j0 + i);
+            rank += o < v ? 1u : 0u;
+        }
     }
     uint64_t* t = lds_wsort();
     if (lane < n) t[rank] = v;
@@ -1254,34 +1283,50 @@ __device__ __forceinline__ Pick wave_finalize(float y, uint32_t id, uint32_t len
         const uint64_t below = wave_ballot(lane < len && !(p >= P.min_p));
         if (below) len = max(static_cast<uint32_t>(__builtin_ctzll(below)), 1u);
     }
+    // The three folds run over the list in steps of eight lanes, without a
+    // branch per element: each records its running value in the lane of the
+    // element just added, and the first lane that meets a condition is found
+    // by ballot afterwards.  Past the list p is 0, which leaves a running sum
+    // as it is (sums of non-negative terms start from +0).
+    const float pl = lane < len ? p : 0.0f;
     // prefix sums (left fold) of p over the list
     float total = 0.0f, pre = 0.0f;
-    for (uint32_t j = 0; j < len; j++) {
-        total += readlane_f(p, j);
-        pre = lane == j ? total : pre;
+    for (uint32_t j0 = 0; j0 < len; j0 += 8) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            total += readlane_f(pl, j0 + i);
+            pre = lane == j0 + i ? total : pre;
+        }
     }
     uint32_t keep = len;
     if (!(m.greedy || P.top_p >= 1.0f)) {
-        const float q = lane < len ? p / total : 0.0f;
-        float acc = 0.0f;
-        for (uint32_t j = 0; j < len; j++) {
-            acc += readlane_f(q, j);
-            if (acc >= P.top_p) {
-                keep = j + 1;
-                break;
+        // the first j with q_0 + ... + q_j >= top_p (sampler.rs:240-246)
+        const float q = lane < len ? pl / total : 0.0f;
+        float acc = 0.0f, accl = 0.0f;
+        for (uint32_t j0 = 0; j0 < len; j0 += 8) {
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                acc += readlane_f(q, j0 + i);
+                accl = lane == j0 + i ? acc : accl;
             }
         }
+        const uint64_t hit = wave_ballot(lane < len && accl >= P.top_p);
+        if (hit) keep = static_cast<uint32_t>(__builtin_ctzll(hit)) + 1u;
     }
     const float mass = readlane_f(pre, keep - 1);
+    // the draw: the first j < keep where u * mass - p_0 - ... - p_j <= 0
+    // (sampler.rs:142-150), else the last kept
     uint32_t pick = keep - 1;
-    float r = u * mass;
-    for (uint32_t j = 0; j < keep; j++) {
-        r -= readlane_f(p, j);
-        if (r <= 0.0f) {
-            pick = j;
-            break;
+    float r = u * mass, rl = 0.0f;
+    for (uint32_t j0 = 0; j0 < keep; j0 += 8) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            r -= readlane_f(pl, j0 + i);
+            rl = lane == j0 + i ? r : rl;
         }
     }
+    const uint64_t hit = wave_ballot(lane < keep && rl <= 0.0f);
+    if (hit) pick = static_cast<uint32_t>(__builtin_ctzll(hit));
     Pick out;
     out.token = wave_read(id, pick);
     out.keep = keep;
@@ -1382,7 +1427,10 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
     // reference: the largest of its threads')
     const uint32_t nallow_w = wave_sum_dpp(nallow);
     const float mref = wave_max_dpp(lsum > 0.0 ? lref : -INFINITY);
-    double sw = lsum > 0.0 ? lsum * exp(static_cast<double>(lref) - static_cast<double>(mref)) : 0.0;
+    // (the rescale factors are f32 exponentials: a term's relative error is
+    // about |exponent| * 2^-24 while its size is 2^exponent, far inside the
+    // logprob tolerance; an f64 exp costs each of the 16 waves ~100 VALU)
+    double sw = lsum > 0.0 ? lsum * static_cast<double>(__builtin_amdgcn_exp2f((lref - mref) * kL2E)) : 0.0;
     sw = wave_sum_f64_dpp(sw);
     best = wave_min_u64_dpp(best);
     if (lane == 0) {
@@ -1431,7 +1479,7 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
         double term = 0.0;
         if (lane < NW) {
             const float mw = __uint_as_float(tmp[3 * NW + lane]);
-            if (mw != -INFINITY) term = md[lane] * exp(static_cast<double>(mw) - static_cast<double>(rmax));
+            if (mw != -INFINITY) term = md[lane] * static_cast<double>(__builtin_amdgcn_exp2f((mw - rmax) * kL2E));
         }
         lse = rmax + static_cast<float>(log(wave_sum_f64_dpp(term)));
     }
@@ -1547,23 +1595,38 @@ template <bool kVecLoads>
 __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const uint32_t n = a.usable;
-    // first the loads nothing waits for: the first two tiles' logits, the row's
-    // history offsets and parameters and its uniform, then its history ids
-    // (every later load waits on one of these; requested together, their
-    // latencies overlap)
+    // first the loads that depend on nothing: the row's history offsets,
+    // parameters and uniform, then the first two tiles' logits.  Loads
+    // complete in order, so the small ones go first: the history ids and mask
+    // words that depend on them can then be requested while the tiles are
+    // still in flight.
+    // The mask words are read whenever the batch has a mask (used only for
+    // constrained rows), else from the logits, in place.
     float v[kVec][4], vB[kVec][4], vC[kVec][4];
     uint32_t mw[kVec], mwB[kVec], mwC[kVec];
     const float* rowp0 = a.logits + static_cast<size_t>(row) * a.row_stride;
-    load_logits<kVecLoads>(rowp0, 0, n, v);
-    load_logits<kVecLoads>(rowp0, kTile, n, vB);
-    uint32_t h0 = 0, hlen = 0;
-    if (a.hist_off) {
-        h0 = a.hist_off[row];
-        const uint32_t h1 = a.hist_off[row + 1];
-        hlen = h1 > h0 ? h1 - h0 : 0u;
+    const uint32_t* hop = a.hist_off ? a.hist_off + row : kZeroWords;
+    const uint32_t h0 = const_as(hop)[0], h1 = const_as(hop)[1];
+    tsm_row_params P;
+    {
+        static_assert(sizeof(tsm_row_params) % 4 == 0, "row parameters are whole words");
+        constexpr int kW = sizeof(tsm_row_params) / 4;
+        const TSM_CONST_AS uint32_t* pw = const_as(reinterpret_cast<const uint32_t*>(a.params + row));
+        uint32_t w[kW];
+#pragma unroll
+        for (int i = 0; i < kW; i++) w[i] = pw[i];
+        __builtin_memcpy(&P, w, sizeof(P));
     }
-    const tsm_row_params P = a.params[row];
-    const float u_row = (a.uniforms && !a.distribution) ? a.uniforms[row] : 0.0f;
+    const float u_load =
+        __uint_as_float(const_as(a.uniforms ? reinterpret_cast<const uint32_t*>(a.uniforms) + row : kZeroWords)[0]);
+    const uint32_t* mp = a.mask ? a.mask + static_cast<size_t>(row) * a.mask_stride
+                                : reinterpret_cast<const uint32_t*>(rowp0);
+    load_logits<kVecLoads>(rowp0, 0, n, v);
+    load_mask(mp, 0, n, mw);
+    load_logits<kVecLoads>(rowp0, kTile, n, vB);
+    load_mask(mp, kTile, n, mwB);
+    const float u_row = a.distribution ? 0.0f : u_load;
+    const uint32_t hlen = h1 > h0 ? h1 - h0 : 0u;
     uint32_t hid[kHistPerThread];
 #pragma unroll
     for (uint32_t k = 0; k < kHistPerThread; k++) {
@@ -1582,7 +1645,6 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     f.P = P;
     const RowMode m = f.m;  // register copies: f escapes to the re-read functions
     const float* rowp = f.rowp;
-    const uint32_t* mrow = f.mrow;
     uint32_t* misc = lds_misc();
     uint2* buf = lds_buf();
     uint2* pen = lds_pen();
@@ -1617,13 +1679,9 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     }
     // three register sets take the tiles in turn (tile t in set t mod 3):
     // tiles t+1 and t+2 are in flight while tile t is processed, and no set is
-    // ever copied to another (a copy would wait for its loads).  The mask
-    // words are read unconditionally, from the logits when there is no mask
-    // (loads past the row's last tile read in bounds and go unused: an
-    // unconditional load keeps one code path).
-    const uint32_t* mp = mrow ? mrow : reinterpret_cast<const uint32_t*>(rowp);
-    load_mask(mp, 0, n, mw);
-    load_mask(mp, kTile, n, mwB);
+    // ever copied to another (a copy would wait for its loads).  Loads past
+    // the row's last tile read in bounds and go unused: an unconditional load
+    // keeps one code path.
     if (pen_lookup) history_build(hid, n);  // barriers inside
 
     SHist sh;
@@ -1725,6 +1783,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                     uint32_t (&mpf)[kVec]) __attribute__((always_inline)) {
         const uint32_t tb = t * kTile;
         load_tile<kVecLoads>(rowp, mp, tb + 2 * kTile, n, pf, mpf);
+        tile_arrived(v, mw);
         mask_tail(v, tb, n);
         // the thresholds as they are now (they only rise, so any value read is
         // valid), loaded before the tile's arithmetic so it hides their latency
@@ -1803,13 +1862,18 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             }
         }
     };
-    for (uint32_t t = 1; t < ntiles; t += 3) {
+    // whole rounds of three tiles, then the one or two left: a break inside
+    // the round would let the compiler's wait analysis see a path from a
+    // round's first tile back to the loop head, and the head would then wait
+    // for that tile's prefetch on every round
+    uint32_t t = 1;
+    for (; t + 2 < ntiles; t += 3) {
         step(t, vB, mwB, v, mw);
-        if (t + 1 >= ntiles) break;
         step(t + 1, vC, mwC, vB, mwB);
-        if (t + 2 >= ntiles) break;
         step(t + 2, v, mw, vC, mwC);
     }
+    if (t < ntiles) step(t, vB, mwB, v, mw);
+    if (t + 1 < ntiles) step(t + 1, vC, mwC, vB, mwB);
     TSM_LDS_SYNC();
     uint32_t bufn = 0;
     if (tracking) {
