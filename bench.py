@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the batched sampling path on one MI355X.
 
-A step is one tsm_sample() call (sweep + finalize kernels) over one batch of
+A step is one tsm_sample() call (one sample_kernel launch) over one batch of
 synthetic logits already resident in HBM.  The default workload is BASELINE
 config c4, the headline: B=256, V=151936, repetition 1.1 + presence 0.4 +
 frequency 0.2 over 1024-token Zipf histories, a 30% grammar mask, T=0.7,
@@ -13,6 +13,10 @@ the stream the kernels run on.  The CPU baseline is the oracle restatement of
 the reference sampler, timed on this host's cores on the same workload.
 
 Prints ONE JSON line.
+
+``--calib-copy-mb N`` instead runs a few device-to-device copies of N MiB
+(reads and writes exactly N MiB each): the run that fixes the scale of the
+rocprofv3 FETCH_SIZE / WRITE_SIZE counters for tachyon_amd/traffic.py.
 """
 from __future__ import annotations
 
@@ -67,6 +71,8 @@ def main():
     ap.add_argument("--sets", type=int, default=3, help="rotated input sets")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="run N MiB device copies for counter calibration instead of the bench")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -74,6 +80,17 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.calib_copy_mb:
+        n = args.calib_copy_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {args.calib_copy_mb} MiB x5")
+        return
 
     from tachyon_amd import workloads as wl
     from tachyon_amd.device import Outputs, SamplerContext, upload
