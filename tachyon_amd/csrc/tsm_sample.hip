@@ -1506,12 +1506,41 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             *c = composite(canon_key(__uint_as_float(wl[r].x)), wl[r].y & kEntId);
             return true;
         };
-        // the window boundary: the W-th best by IEEE order (top_n, sampler.rs:192-194)
-        const uint64_t tw = wave_kth_reg(nwin, m.window, canon_all);
+        auto allowed_c = [&](uint32_t r, uint64_t* c) {
+            if (!(wl[r].y & kEntAllowed)) return false;
+            return canon_all(r, c);
+        };
+        // A constrained row keeps the `want` best allowed ids of the window
+        // when the window holds at least that many (sampler.rs:209-210,
+        // :223).  Those are then the `want` best allowed ids of the row: the
+        // want-th of them, ta, decides it alone when at most W listed
+        // entries rank at or above it (every element at or above the window
+        // threshold is listed, so the count is the rank of ta in the row
+        // whenever it is <= W), and the window boundary is not needed.
+        uint64_t ta = ~0ull;
+        bool fast = false;
+        if (m.constrained) {
+            ta = wave_kth_reg(nwin, m.want, allowed_c);
+            if (ta != ~0ull) {
+                uint32_t rank = 0;
+#pragma unroll
+                for (uint32_t r = 0; r < kWaveRegs; r++) {
+                    if (r * kWave >= nwin) break;
+                    uint64_t c;
+                    rank += (r * kWave + lane < nwin && canon_all(r, &c) && c <= ta) ? 1u : 0u;
+                }
+                fast = wave_sum_dpp(rank) <= m.window;
+            }
+        }
         uint32_t g;
-        if (!m.constrained) {
+        if (fast) {
+            g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return allowed_c(r, c) && *c <= ta; });
+        } else if (!m.constrained) {
+            // the window boundary: the W-th best by IEEE order (top_n, sampler.rs:192-194)
+            const uint64_t tw = wave_kth_reg(nwin, m.window, canon_all);
             g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return canon_all(r, c) && *c <= tw; });
         } else {
+            const uint64_t tw = wave_kth_reg(nwin, m.window, canon_all);
             // allowed ids inside the window (sampler.rs:209-210)
             auto in_window = [&](uint32_t r, uint64_t* c) {
                 if (!(wl[r].y & kEntAllowed)) return false;
@@ -1526,8 +1555,8 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             }
             inw = wave_sum_dpp(inw);
             if (inw > 0) {
-                const uint64_t ta = inw > m.want ? wave_kth_reg(nwin, m.want, in_window) : ~0ull;
-                g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return in_window(r, c) && *c <= ta; });
+                const uint64_t tin = inw > m.want ? wave_kth_reg(nwin, m.want, in_window) : ~0ull;
+                g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return in_window(r, c) && *c <= tin; });
             } else {
                 // none in the window: the best allowed ids of the whole row by
                 // f32::total_cmp (sampler.rs:211-221)
@@ -1572,9 +1601,16 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             *c = rl[r];
             return true;
         };
-        const uint64_t tr = wave_kth_reg(nraw_all, nlp, raw_key);
-        const uint32_t g = wave_gather_reg(nraw_all, [&](uint32_t r, uint64_t* c) { return raw_key(r, c) && *c <= tr; });
-        const uint64_t mine = wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
+        uint64_t mine;
+        uint32_t g;
+        if (nraw_all <= static_cast<uint32_t>(kWave)) {  // one entry per lane: rank them all
+            g = nraw_all;
+            mine = wave_sort_rank(rl[0], g);
+        } else {
+            const uint64_t tr = wave_kth_reg(nraw_all, nlp, raw_key);
+            g = wave_gather_reg(nraw_all, [&](uint32_t r, uint64_t* c) { return raw_key(r, c) && *c <= tr; });
+            mine = wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
+        }
         const uint32_t nraw = min(g, nlp);
         if (lane < nraw) {
             const size_t o = static_cast<size_t>(row) * a.top_stride + lane;
