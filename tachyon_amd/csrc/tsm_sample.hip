@@ -483,55 +483,92 @@ __device__ __forceinline__ uint32_t wave_lane_bound(uint32_t lm, uint32_t need) 
     return k;
 }
 
+// Key distances below the first tile's largest key, in bins of 1/8 octave:
+// distances 0..7 exactly, then for d in [2^e, 2^(e+1)) the bin (e-2)*8 + the
+// three bits after the leading one (240 bins up to d < 2^32).
+constexpr uint32_t kDistBins = 240;
+__device__ __forceinline__ uint32_t dist_bin(uint32_t d) {
+    if (d < 8u) return d;
+    const uint32_t e = 31u - static_cast<uint32_t>(__builtin_clz(d));
+    return ((e - 2u) << 3) | ((d >> (e - 3u)) & 7u);
+}
+// The largest distance that falls in bin b.
+__device__ __forceinline__ uint64_t dist_hi(uint32_t b) {
+    if (b < 8u) return b;
+    const uint32_t e = (b >> 3) + 2u;
+    return ((static_cast<uint64_t>(9u + (b & 7u))) << (e - 3u)) - 1u;
+}
+
 // Lower bounds for the thresholds from the first tile: k[g] is this thread's
-// largest key among its 8 ids relevant to target g (0: none).  For each
-// target the group maxima are histogrammed on the 11 bits below the prefix
-// they all share; the digit of the need-th largest gives a value with at
-// least `need` of the tile's elements at or above it, which raises
-// misc[M_THR + g].  top[g] gets the largest canon key among the tile's
-// elements relevant to target g (0: none).  Block-wide, ends with a barrier.
-__device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t top[3]) {
-    const uint32_t tid = threadIdx.x;
-    uint32_t* h3 = lds_hist3();
-    uint32_t* misc = lds_misc();
+// largest key among its 8 ids relevant to target g (0: none), so the k[g] are
+// distinct elements of the row.  For each target the block's largest k[g]
+// (kmax) is found, the distances kmax - k[g] are histogrammed (dist_bin),
+// and the bin where the count from the top reaches need[g] gives a key with
+// at least need[g] of these elements at or above it.  key[g] gets the target's
+// threshold (a canon key, the larger of that bound and the target's start),
+// top[g] the largest canon key among the tile's elements relevant to target g
+// (0: none); thread 0 stores the thresholds in misc[M_THR + g], visible after
+// the caller's next barrier.  Block-wide, two barriers; every wave finds the
+// bins itself, so no third barrier hands the result over.
+__device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t key[3],
+                                            uint32_t top[3]) {
+    constexpr uint32_t NW = kBlock / kWave;
+    static_assert(3 * kDistBins <= kBlock && 4 * kWave >= kDistBins, "bin layout");
+    const uint32_t tid = threadIdx.x, lane = lane_id(), wid = tid / kWave;
+    uint32_t* h = lds_hist3();
+    uint32_t* tmp = lds_tmp();
     const uint32_t k[3] = {k0, k1, k2};
-    unsigned long long mn[3], mx[3];  // over ~key of the non-empty groups
+    if (tid < 3 * kDistBins) h[tid] = 0;
 #pragma unroll
     for (int g = 0; g < 3; g++) {
-        mn[g] = (tg.need[g] && k[g]) ? static_cast<unsigned long long>(~k[g]) : ~0ull;
-        mx[g] = (tg.need[g] && k[g]) ? static_cast<unsigned long long>(~k[g]) : 0ull;
+        const uint32_t wm = wave_max_u32(tg.need[g] ? k[g] : 0u);
+        if (lane == 0) tmp[g * NW + wid] = wm;
     }
-    block_minmax3(mn, mx);
-    int lo[3], tb[3];
-#pragma unroll
-    for (int g = 0; g < 3; g++) {
-        tb[g] = mn[g] <= mx[g] ? high_bit64(mn[g] ^ mx[g]) + 1 : 0;
-        lo[g] = tb[g] > 11 ? tb[g] - 11 : 0;
-        top[g] = mn[g] <= mx[g] ? canon_key(key_to_float(~static_cast<uint32_t>(mn[g]))) : 0u;
-    }
-    for (uint32_t i = tid; i < 3 * kBins; i += kBlock) h3[i] = 0;
     TSM_LDS_SYNC();
+    uint32_t kmax[3];
+#pragma unroll
+    for (int g = 0; g < 3; g++) kmax[g] = row_max16(lane < NW ? tmp[g * NW + lane] : 0u);
 #pragma unroll
     for (int g = 0; g < 3; g++)
-        if (tg.need[g] && k[g] != 0u)
-            atomicAdd(&h3[g * kBins + (((~k[g]) >> lo[g]) & ((1u << (tb[g] - lo[g])) - 1u))], 1u);
+        if (tg.need[g] && k[g] != 0u) atomicAdd(&h[g * kDistBins + dist_bin(kmax[g] - k[g])], 1u);
     TSM_LDS_SYNC();
-    hist_find3(tg.need);
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+        key[g] = tg.need[g] ? kKeyNegInf : kKeyUntracked;
+        top[g] = kmax[g] ? canon_key(key_to_float(kmax[g])) : 0u;
+        if (!tg.need[g] || kmax[g] == 0u) continue;
+        // lane l holds bins 4l .. 4l+3, smallest distance first
+        uint32_t c[4], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t bi = 4u * lane + i;
+            c[i] = bi < kDistBins ? h[g * kDistBins + bi] : 0u;
+            sum += c[i];
+        }
+        const uint32_t incl = wave_incl_scan(sum);
+        const uint64_t hit = wave_ballot(incl >= tg.need[g]);
+        if (hit == 0) continue;  // fewer relevant elements than need: no bound
+        uint32_t run = incl - sum, bin = 0;
+        bool done = false;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (!done && run + c[i] >= tg.need[g]) {
+                bin = 4u * lane + i;
+                done = true;
+            }
+            run += c[i];
+        }
+        bin = wave_read(bin, static_cast<uint32_t>(__builtin_ctzll(hit)));
+        const uint64_t hi = dist_hi(bin);
+        if (hi >= kmax[g]) continue;
+        const uint32_t kb = kmax[g] - static_cast<uint32_t>(hi);
+        const float b = kb <= 0x007FFFFFu ? -INFINITY : key_to_float(kb);
+        key[g] = max(key[g], canon_key(b));
+    }
     if (tid == 0) {
 #pragma unroll
-        for (int g = 0; g < 3; g++) {
-            const uint32_t d = misc[M_SEL + 2 * g];
-            if (tg.need[g] && d != 0xFFFFFFFFu) {
-                // the bin's largest ~key (its lowest key): shared prefix, digit, ones below
-                const uint32_t pre = tb[g] >= 32 ? 0u : (static_cast<uint32_t>(mn[g]) >> tb[g]) << tb[g];
-                const uint32_t nk = pre | (d << lo[g]) | ((1u << lo[g]) - 1u);
-                const uint32_t key = ~nk;
-                const float b = key <= 0x007FFFFFu ? -INFINITY : key_to_float(key);
-                misc[M_THR + g] = max(misc[M_THR + g], canon_key(b));
-            }
-        }
+        for (int g = 0; g < 3; g++) lds_misc()[M_THR + g] = key[g];
     }
-    TSM_LDS_SYNC();
 }
 
 // Loads one tile into registers.  With vector loads (row_stride a multiple of
@@ -1766,14 +1803,10 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                     if ((fl.al >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
                 }
                 k[SK_RAW] = k[SK_ALL];  // the stream's candidates are the non-penalized ids
-                uint32_t top[3];
-                tile_bounds(tg, k[0], k[1], k[2], top);
-                uint32_t key[3];
+                uint32_t top[3], key[3];
+                tile_bounds(tg, k[0], k[1], k[2], key, top);
 #pragma unroll
-                for (int g = 0; g < 3; g++) {
-                    key[g] = misc[M_THR + g];
-                    th[g] = thr_float(key[g]);
-                }
+                for (int g = 0; g < 3; g++) th[g] = thr_float(key[g]);
                 // histogram geometry: H[0] from the all / raw bounds; H[1] from
                 // the allowed bound, or H[0]'s when the first tile gave none
                 uint32_t b0 = kKeyUntracked, t0 = 0;
