@@ -704,8 +704,8 @@ struct TileFlags {
 };
 
 __device__ __forceinline__ TileFlags tile_prep(const float (&v)[kVec][4], const uint32_t (&mw)[kVec], uint32_t tb,
-                                               uint32_t n, bool logprobs, bool pen_lookup, bool track_pen,
-                                               bool constrained, LseAcc& L, uint32_t& nallow) {
+                                               uint32_t n, bool logprobs, bool pen_lookup, bool constrained,
+                                               LseAcc& L, uint32_t& nallow) {
     const uint32_t tid = threadIdx.x;
     uint32_t valid = (1u << (kVec * 4)) - 1u;
     if (tb + kTile > n) {  // the row's last, partial tile
@@ -747,20 +747,6 @@ __device__ __forceinline__ TileFlags tile_prep(const float (&v)[kVec][4], const 
     pen &= valid;
     al &= valid;
     nallow += __popc(al);
-    if (track_pen && pen) {
-        // static element indices: an indexed read of v would put the tile in
-        // scratch memory, whose accesses wait on the prefetch loads
-        uint32_t* misc = lds_misc();
-#pragma unroll
-        for (int e = 0; e < kVec * 4; e++)
-            if ((pen >> e) & 1u) {
-                const uint32_t pos = atomicAdd(&misc[M_PENN], 1u);
-                if (pos < kPenCap)
-                    lds_pen()[pos] = make_uint2(__float_as_uint(v[e >> 2][e & 3]),
-                                                (tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3u)) |
-                                                    (((al >> e) & 1u) ? kEntAllowed : 0u));
-            }
-    }
     TileFlags fl;
     fl.elig = valid & ~pen;
     fl.valid = valid;
@@ -1756,6 +1742,30 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     // the row's last tile read in bounds and go unused: an unconditional load
     // keeps one code path.
     if (pen_lookup) history_build(hid, n);  // barriers inside
+    // The penalized list (raw logit, id, allowed bit) is gathered once, from
+    // the history table's distinct ids: each thread loads the logits and mask
+    // words of its table slots now and files them after the first tile, when
+    // the loads have long arrived; the stream itself only skips penalized ids.
+    constexpr uint32_t kSlotsPerThread = kHashSlots / kBlock;
+    static_assert(kSlotsPerThread * kBlock == kHashSlots, "table slots per thread");
+    float pen_x[kSlotsPerThread];
+    uint32_t pen_w[kSlotsPerThread], pen_id[kSlotsPerThread];
+#pragma unroll
+    for (uint32_t k = 0; k < kSlotsPerThread; k++) {
+        pen_x[k] = 0.0f;
+        pen_w[k] = 0u;
+        pen_id[k] = 0xFFFFFFFFu;
+    }
+    if (track_pen) {
+#pragma unroll
+        for (uint32_t k = 0; k < kSlotsPerThread; k++) {
+            const uint32_t key = lds_hkey()[tid + k * kBlock];  // id + 1, 0 = empty
+            pen_id[k] = key - 1u;
+            const uint32_t id = key ? key - 1u : 0u;
+            pen_x[k] = rowp[id];
+            pen_w[k] = mp[id >> 5];
+        }
+    }
 
     SHist sh;
     sh.base[0] = sh.base[1] = kKeyUntracked;
@@ -1781,7 +1791,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     {
         // first tile: block-wide, so the thresholds can start from the tile's
         // own group-max bounds
-        const TileFlags fl = tile_prep(v, mw, 0, n, m.logprobs, pen_lookup, track_pen, m.constrained, lse, nallow);
+        const TileFlags fl = tile_prep(v, mw, 0, n, m.logprobs, pen_lookup, m.constrained, lse, nallow);
         if (tracking) {
             float th[3];
 #pragma unroll
@@ -1842,6 +1852,28 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                     buf[pos++] = make_entry(y, 4u * ((e >> 2) * kBlock + tid) + (e & 3), 0u, fl.al, e);
                     if (bound) count_kept(y, (fl.al >> e) & 1u, sh);
                 }
+            if (track_pen) {
+                // one LDS atomic per wave reserves the wave's places
+                uint64_t b[kSlotsPerThread];
+                uint32_t cnt = 0;
+#pragma unroll
+                for (uint32_t k = 0; k < kSlotsPerThread; k++) {
+                    b[k] = wave_ballot(pen_id[k] != 0xFFFFFFFFu);
+                    cnt += static_cast<uint32_t>(__popcll(b[k]));
+                }
+                uint32_t at = 0;
+                if (cnt && lane == 0) at = atomicAdd(&misc[M_PENN], cnt);
+                at = wave_uniform(wave_read(at, 0));
+#pragma unroll
+                for (uint32_t k = 0; k < kSlotsPerThread; k++) {
+                    const uint32_t id = pen_id[k];
+                    if (id != 0xFFFFFFFFu) {
+                        const bool al = m.constrained && ((pen_w[k] >> (id & 31u)) & 1u);
+                        pen[at + lanes_below(b[k])] = make_uint2(__float_as_uint(pen_x[k]), id | (al ? kEntAllowed : 0u));
+                    }
+                    at += static_cast<uint32_t>(__popcll(b[k]));
+                }
+            }
             seg0 = total;
             seg_cap = ((kBufCap - total) / (kBlock / kWave)) & ~1u;
             TSM_LDS_SYNC();
@@ -1863,7 +1895,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             kR = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]);
             kL = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)]);
         }
-        const TileFlags fl = tile_prep(v, mw, tb, n, m.logprobs, pen_lookup, track_pen, m.constrained, lse, nallow);
+        const TileFlags fl = tile_prep(v, mw, tb, n, m.logprobs, pen_lookup, m.constrained, lse, nallow);
         if (wave_track && wave_uniform(ovf) != 0u) wave_track = false;  // the finish re-reads the row
         if (wave_track) {
             // no barriers: each wave appends to its own segment and publishes
