@@ -1,8 +1,10 @@
 """Builds the HIP sampling library for gfx950, in tree.
 
 Outputs (next to this file):
-  lib/libtachyon_sampler.so  - shared library (ctypes, C++ callers)
-  lib/libtachyon_sampler.a   - static archive (what a Rust build.rs links)
+  lib/libtachyon_sampler.so       - shared library (ctypes, C++ callers)
+  lib/libtachyon_sampler.a        - static archive (what a Rust build.rs links)
+  lib/libtachyon_sampler_host.a   - the C++ Sampler API over the C ABI (host/)
+and, with build_host_tests(), tests/host/test_sampler_host.
 
 hipcc flags: -O3 for gfx950 only; -ffp-contract=off so every float/double
 operation rounds on its own (the sampler's f32 arithmetic is reproduced bit
@@ -74,6 +76,47 @@ def build_test_helpers(verbose: bool = False) -> str:
     src = os.path.join(d, "tsm_probe.hip")
     out = os.path.join(d, "libtsm_probe.so")
     cmd = [HIPCC, *DEVICE_FLAGS, "-shared", src, "-o", out + ".tmp"]
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+# The C++ layer is host code over the HIP runtime API: g++, no device pass.
+CXX = os.environ.get("CXX", "g++")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+              "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROCM, "include")]
+
+
+def build_host(verbose: bool = False) -> str:
+    """The C++ Sampler API (host/sampler.cpp) as a static archive."""
+    os.makedirs(LIBDIR, exist_ok=True)
+    obj = os.path.join(LIBDIR, "sampler_host.o")
+    cmd = [CXX, *HOST_FLAGS, "-c", os.path.join(HERE, "host", "sampler.cpp"), "-o", obj]
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    a = os.path.join(LIBDIR, "libtachyon_sampler_host.a")
+    if os.path.exists(a):
+        os.remove(a)
+    _run([shutil.which("ar") or "ar", "crs", a, obj])
+    return a
+
+
+def build_host_tests(verbose: bool = False) -> str:
+    """tests/host/test_sampler_host: the C++ API's tests, linked with the
+    library, its C++ layer and the CPU oracle (the checker)."""
+    host_a = build_host(verbose)
+    d = os.path.join(ROOT, "tests", "host")
+    out = os.path.join(d, "test_sampler_host")
+    oracle_dir = os.path.join(ROOT, "oracle")
+    cmd = [CXX, *HOST_FLAGS, os.path.join(d, "test_sampler_host.cpp"), host_a,
+           "-L", LIBDIR, "-ltachyon_sampler", "-L", oracle_dir, "-ltachyon_oracle",
+           "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN/../../tachyon_amd/lib", "-Wl,-rpath,$ORIGIN/../../oracle",
+           f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}", "-o", out + ".tmp"]
     if verbose:
         print(" ".join(cmd))
     _run(cmd)
