@@ -507,11 +507,13 @@ __device__ __forceinline__ uint64_t dist_hi(uint32_t b) {
 // at least need[g] of these elements at or above it.  key[g] gets the target's
 // threshold (a canon key, the larger of that bound and the target's start),
 // top[g] the largest canon key among the tile's elements relevant to target g
-// (0: none); thread 0 stores the thresholds in misc[M_THR + g], visible after
+// (0: none), *low a canon key at or below every group maximum of target 0
+// (the bottom of the tile's range, for histogram geometry; 0: none); thread 0
+// stores the thresholds in misc[M_THR + g], visible after
 // the caller's next barrier.  Block-wide, two barriers; every wave finds the
 // bins itself, so no third barrier hands the result over.
 __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t key[3],
-                                            uint32_t top[3]) {
+                                            uint32_t top[3], uint32_t* low) {
     constexpr uint32_t NW = kBlock / kWave;
     static_assert(3 * kDistBins <= kBlock && 4 * kWave >= kDistBins, "bin layout");
     const uint32_t tid = threadIdx.x, lane = lane_id(), wid = tid / kWave;
@@ -532,6 +534,7 @@ __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1
     for (int g = 0; g < 3; g++)
         if (tg.need[g] && k[g] != 0u) atomicAdd(&h[g * kDistBins + dist_bin(kmax[g] - k[g])], 1u);
     TSM_LDS_SYNC();
+    *low = 0u;
 #pragma unroll
     for (int g = 0; g < 3; g++) {
         key[g] = tg.need[g] ? kKeyNegInf : kKeyUntracked;
@@ -546,6 +549,17 @@ __device__ __forceinline__ void tile_bounds(Targets tg, uint32_t k0, uint32_t k1
             sum += c[i];
         }
         const uint32_t incl = wave_incl_scan(sum);
+        if (g == 0) {
+            // the largest distance any group maximum has: the bottom of the range
+            uint32_t hb = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (c[i]) hb = 4u * lane + i;
+            hb = wave_max_u32(hb);
+            const uint64_t hhi = dist_hi(hb);
+            const uint32_t kl = hhi >= kmax[0] ? 0u : kmax[0] - static_cast<uint32_t>(hhi);
+            *low = kl <= 0x007FFFFFu ? kKeyNegInf : canon_key(key_to_float(kl));
+        }
         const uint64_t hit = wave_ballot(incl >= tg.need[g]);
         if (hit == 0) continue;  // fewer relevant elements than need: no bound
         uint32_t run = incl - sum, bin = 0;
@@ -1036,7 +1050,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in,
 // through LDS between wave barriers (the wave runs in lockstep; the barrier
 // keeps the compiler from reordering across it).
 constexpr uint32_t kWaveList = 64;                  // longest ranked list the wave finish takes
-constexpr uint32_t kListCap = kBufCap;              // entries of each filtered list
+constexpr uint32_t kListCap = 1024;                 // entries of each filtered list (the wave finish takes no more)
 __device__ __forceinline__ uint2* lds_swin() { return reinterpret_cast<uint2*>(lds_base()); }  // region A
 __device__ __forceinline__ uint64_t* lds_sraw() { return reinterpret_cast<uint64_t*>(lds_base() + kListCap * 8); }
 __device__ __forceinline__ uint32_t* lds_whist() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHist); }
@@ -1146,6 +1160,7 @@ __device__ uint64_t wave_kth(uint32_t n, uint32_t k, KeyOf key_of) {
 // in slot r = i / 64 of lane i % 64 (kWaveRegs slots per lane).
 constexpr uint32_t kWaveRegs = 16;
 constexpr uint32_t kWaveRegCap = kWaveRegs * kWave;
+static_assert(kWaveRegCap <= kListCap, "a list that fits the wave's registers fits its LDS list");
 
 // wave_kth over a register list: key_of(r, &c) gives the key of this lane's
 // slot r (false: not in the set); slots at or past n are never asked.
@@ -1813,8 +1828,8 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                     if ((fl.al >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
                 }
                 k[SK_RAW] = k[SK_ALL];  // the stream's candidates are the non-penalized ids
-                uint32_t top[3], key[3];
-                tile_bounds(tg, k[0], k[1], k[2], key, top);
+                uint32_t top[3], key[3], low;
+                tile_bounds(tg, k[0], k[1], k[2], key, top, &low);
 #pragma unroll
                 for (int g = 0; g < 3; g++) th[g] = thr_float(key[g]);
                 // histogram geometry: H[0] from the all / raw bounds; H[1] from
@@ -1831,6 +1846,15 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                 if (tg.need[SK_ALLOWED] && key[SK_ALLOWED] > kKeyNegInf) {
                     sh.base[1] = key[SK_ALLOWED];
                     sh.shift[1] = geo_shift(key[SK_ALLOWED], top[SK_ALLOWED]);
+                } else if (tg.need[SK_ALLOWED] && b0 > low && t0 > b0) {
+                    // too few allowed ids in the first tile to bound them: the
+                    // allowed histogram reaches three spans of the window
+                    // histogram further down (not below the tile's lowest
+                    // group maximum), so allowed candidates below the other
+                    // thresholds are still counted
+                    const uint64_t ext = min(3ull * (t0 - b0), static_cast<uint64_t>(b0 - low));
+                    sh.base[1] = b0 - static_cast<uint32_t>(ext);
+                    sh.shift[1] = geo_shift(sh.base[1], t0);
                 } else {
                     sh.base[1] = sh.base[0];
                     sh.shift[1] = sh.shift[0];
@@ -1936,6 +1960,18 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                 tot = count();
             }
             if (tot) {
+                if (seg_fill + tot > seg_cap) {
+                    // the segment cannot take the tile's candidates: raise the
+                    // thresholds from everything published so far (any wave
+                    // may raise), then count again before giving up
+                    count_published(sh, seg0, seg_cap);
+                    raise_thresholds(tg, sh);
+                    tAR = fminf(thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)]))),
+                                thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]))));
+                    tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
+                    use_l = !(tL >= tAR) && tL == tL;
+                    tot = count();
+                }
                 if (seg_fill + tot <= seg_cap) {
                     const uint32_t pos = seg0 + wid * seg_cap + seg_fill;
                     if (use_l) {

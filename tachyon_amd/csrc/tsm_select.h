@@ -26,7 +26,7 @@ constexpr uint32_t kReTile = 16384;        // ids per tile of a re-read pass
 constexpr uint32_t kBitmapWords = 8192;    // history bitmap: rows of up to 262144 ids
 constexpr uint32_t kHashSlots = 4096;      // history count table (histories up to kHistFast ids)
 constexpr uint32_t kHistFast = kHashSlots / 2;
-constexpr uint32_t kBufCap = 4096;         // candidate buffer entries (y bits, id | flags)
+constexpr uint32_t kBufCap = 6144;         // candidate buffer entries (y bits, id | flags)
 constexpr uint32_t kPenCap = 2048;         // penalized-id list entries (raw x bits, id)
 constexpr uint32_t kOffBitmap = 0;                              // u32[kBitmapWords]
 constexpr uint32_t kOffHashKey = kOffBitmap + kBitmapWords * 4;  // u32[kHashSlots]: id + 1, 0 = empty
