@@ -140,6 +140,17 @@ __device__ __forceinline__ unsigned char* lds_base() {
     return tsm_lds;
 }
 
+// Row data read by the re-read passes: a pointer in the global address space
+// gives global loads (vector memory counter only) where a generic pointer
+// would give flat loads, which also wait on LDS traffic.
+#ifndef TSM_GLOBAL_AS
+#define TSM_GLOBAL_AS __attribute__((address_space(1)))
+#endif
+template <class T>
+__device__ __forceinline__ const TSM_GLOBAL_AS T* global_as(const T* p) {
+    return (const TSM_GLOBAL_AS T*)p;
+}
+
 // Memory the kernel only reads, at addresses uniform over the workgroup (the
 // row's parameters, history offsets and uniform): loads through the constant
 // address space become scalar loads, which count on their own counter, so

@@ -1801,7 +1801,12 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         lse.set_ref(t0 == -INFINITY ? 0.0f : t0);
     }
     uint32_t nallow = 0;
-    const uint32_t ntiles = (n + kTile - 1) / kTile;
+    // the stream's results (candidates, allowed count, logsumexp) serve
+    // top-k rows, constrained rows and logprob rows; any other row (a nucleus
+    // over the whole vocabulary) is finished by re-reading and stops after
+    // the first tile
+    const bool stream_all = tracking || m.logprobs || m.constrained;
+    const uint32_t ntiles = stream_all ? (n + kTile - 1) / kTile : 1u;
     load_tile<kVecLoads>(rowp, mp, 2 * kTile, n, vC, mwC);  // prefetch
     {
         // first tile: block-wide, so the thresholds can start from the tile's

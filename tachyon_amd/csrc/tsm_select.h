@@ -4,10 +4,13 @@
 // ranked candidate list (the reference's sequential f32 arithmetic).
 //
 // A re-read streams the row in 16384-id tiles and answers order-statistic
-// questions with 11-bit LDS radix histograms:
-//   * select_kth: the k-th element in (value desc, id asc) order;
-//   * mass_select: the first element whose cumulative probability reaches a
-//     target (f64 partial sums; used when more than 1024 candidates remain).
+// questions with 11-bit LDS histograms:
+//   * select_kth: the k-th element in (value desc, id asc) order (radix);
+//   * mass selection: the first element whose cumulative probability reaches
+//     a target, with f64 partial sums, used when more than 1024 candidates
+//     remain.  Value bins (counts and masses per bin of (y0 - y) / t) find
+//     the bin that holds the target and one gather resolves it; radix rounds
+//     (mass_select) decide where a bin holds too many equal values.
 // When at most 1024 candidates remain they are gathered, sorted and finished
 // by exact_finalize, which reproduces the CPU sampler's roundings.
 #pragma once
@@ -64,6 +67,7 @@ enum : uint32_t {  // misc word indices
     M_BUFN = 11,    // candidate buffer fill
     M_PENN = 12,    // penalized list fill (may exceed kPenCap: overflow)
     M_FLAGS = 13,   // ROWF_* bits
+    M_VBAD = 14,    // a value-bin pass met a NaN
     M_THR = 16,     // 3 stream thresholds (canon keys): all, raw, allowed
     M_OVF = 19,     // nonzero once a reservation ran past the candidate buffer
     M_SEL = 20,     // 3 x 2 hist_find3 results
@@ -135,32 +139,50 @@ __device__ __forceinline__ bool keep_el(const Fin& f, const Filt& q, uint32_t id
     return true;
 }
 
-// One re-read of the row in tiles; fn(id, raw, penalized) for every id.
-template <class F>
+// One re-read of the row in tiles; fn(id, raw, penalized) for every id.  Each
+// thread loads G elements before it processes them, so G loads are in flight
+// per thread (G > 1 for the passes that dominate a long re-read path).
+template <int G = 1, class F>
 __device__ void row_pass(Fin& f, F&& fn) {
     const uint32_t tid = threadIdx.x;
-    for (uint32_t tb = 0; tb < f.n; tb += kReTile) {
-        const uint32_t tl = min(kReTile, f.n - tb);
-        if (f.m.penal) {
+    const uint32_t n = f.n;
+    const bool penal = f.m.penal;
+    const TSM_GLOBAL_AS float* rowp = global_as(f.rowp);
+    const TSM_GLOBAL_AS uint32_t* hist = global_as(f.hist);
+    const uint32_t hc = min(f.hlen, TSM_MAX_HISTORY);
+    for (uint32_t tb = 0; tb < n; tb += kReTile) {
+        const uint32_t tl = min(kReTile, n - tb);
+        if (penal) {
             TSM_LDS_SYNC();
             for (uint32_t i = tid; i < kReTile / 2; i += kBlock) f.cnt()[i] = 0;
             TSM_LDS_SYNC();
-            const uint32_t hc = min(f.hlen, TSM_MAX_HISTORY);
             for (uint32_t h = tid; h < hc; h += kBlock) {
-                const uint32_t li = f.hist[h] - tb;
+                const uint32_t li = hist[h] - tb;
                 if (li < tl) atomicAdd(&f.cnt()[li >> 1], 1u << ((li & 1u) << 4));
             }
             TSM_LDS_SYNC();
         }
-        for (uint32_t i = tid; i < tl; i += kBlock) {
-            const uint32_t id = tb + i;
-            const float x = f.rowp[id];
-            float y = x;
-            if (f.m.penal) {
-                const uint32_t c = (f.cnt()[i >> 1] >> ((i & 1u) << 4)) & 0xFFFFu;
-                if (c) y = penalize(x, c, f.m, f.P);
+        for (uint32_t i0 = tid; i0 < tl; i0 += G * kBlock) {
+            float xs[G];
+#pragma unroll
+            for (int k = 0; k < G; k++) {
+                const uint32_t i = i0 + static_cast<uint32_t>(k) * kBlock;
+                xs[k] = i < tl ? rowp[tb + i] : 0.0f;
             }
-            fn(id, x, y);
+#pragma unroll
+            for (int k = 0; k < G; k++) {
+                const uint32_t i = i0 + static_cast<uint32_t>(k) * kBlock;
+                if (i < tl) {
+                    const uint32_t id = tb + i;
+                    const float x = xs[k];
+                    float y = x;
+                    if (penal) {
+                        const uint32_t c = (f.cnt()[i >> 1] >> ((i & 1u) << 4)) & 0xFFFFu;
+                        if (c) y = penalize(x, c, f.m, f.P);
+                    }
+                    fn(id, x, y);
+                }
+            }
         }
     }
     TSM_LDS_SYNC();
@@ -192,7 +214,7 @@ __device__ __forceinline__ uint32_t pow2_ceil(uint32_t v) {
 }
 
 // Counts filtered elements (one pass).
-__device__ uint32_t count_pass(Fin& f, const Filt& q) {
+__device__ __forceinline__ uint32_t count_pass(Fin& f, const Filt& q) {
     uint32_t local = 0;
     row_pass(f, [&](uint32_t id, float x, float y) {
         const uint64_t c = comp_of(q.order, id, x, y);
@@ -210,7 +232,7 @@ __constant__ int kRoundW[5] = {11, 11, 10, 11, 11};
 // position `known_lo` fixed to those of `known`.  Returns T such that exactly
 // `need` filtered elements sharing those bits have composite <= T, or ~0 if
 // fewer than `need` exist.
-__device__ uint64_t select_from(Fin& f, const Filt& q, uint32_t need, int r0, uint64_t known,
+__device__ __forceinline__ uint64_t select_from(Fin& f, const Filt& q, uint32_t need, int r0, uint64_t known,
                                 int known_lo) {
     const uint32_t tid = threadIdx.x;
     for (int r = r0; r < 5; r++) {
@@ -246,7 +268,7 @@ __device__ __forceinline__ uint64_t select_kth(Fin& f, const Filt& q, uint32_t k
 // The filtered element with the largest composite <= T, or ~0 when there is
 // none.  select_kth / mass_select return a threshold whose low bits may be
 // padding; this resolves it to the element itself (its id is the low word).
-__device__ uint64_t exact_at(Fin& f, const Filt& q, uint64_t T) {
+__device__ __forceinline__ uint64_t exact_at(Fin& f, const Filt& q, uint64_t T) {
     unsigned long long best = 0;
     uint32_t any = 0;
     row_pass(f, [&](uint32_t id, float x, float y) {
@@ -302,7 +324,9 @@ struct MassSel {
 
 // First filtered element, in (value desc, id asc) order, whose inclusive
 // cumulative p = exp((y - y0) / t) reaches `target`.
-__device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
+__device__ __noinline__ MassSel mass_select(Fin& f_in, const Filt& q_in, float y0, double target) {
+    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
+    const Filt q = q_in;
     const uint32_t tid = threadIdx.x;
     uint64_t known = 0;
     int known_lo = 64;
@@ -380,7 +404,7 @@ __device__ MassSel mass_select(Fin& f, const Filt& q, float y0, double target) {
 }
 
 // Sum of p over the filtered elements (f64) and their count.
-__device__ double mass_total(Fin& f, const Filt& q, float y0) {
+__device__ __forceinline__ double mass_total(Fin& f, const Filt& q, float y0) {
     double local = 0.0;
     row_pass(f, [&](uint32_t id, float x, float y) {
         const uint64_t c = comp_of(q.order, id, x, y);
@@ -392,7 +416,7 @@ __device__ double mass_total(Fin& f, const Filt& q, float y0) {
 }
 
 // Gathers filtered elements' composites into gcomp (caller guarantees <= cap).
-__device__ uint32_t gather_pass(Fin& f, const Filt& q, uint32_t cap) {
+__device__ __forceinline__ uint32_t gather_pass(Fin& f, const Filt& q, uint32_t cap) {
     if (threadIdx.x == 0) f.misc()[M_CNT] = 0;
     TSM_LDS_SYNC();
     row_pass(f, [&](uint32_t id, float x, float y) {
@@ -443,6 +467,192 @@ __device__ void sort_gathered(Fin& f, uint32_t n) {
         f.rid()[j] = static_cast<uint32_t>(c);
     }
     TSM_LDS_SYNC();
+}
+
+constexpr int kNucGroup = 4;  // loads in flight per thread in the nucleus passes
+
+// ---- value-binned mass selection -------------------------------------------------
+// The nucleus of a row without top-k holds up to the whole vocabulary.  Its
+// mass selections (top-p, then the draw among the kept) bin the filtered
+// elements by value: bin(y) = floor((y0 - y) * mul), clamped to [0, kBins).
+// (y0 - y) * mul is monotone in y, so ascending bins visit the elements in
+// (value desc) order and equal values share a bin.  One pass builds the
+// counts and f64 masses p = exp((y - y0) / t) per bin; the bin where the
+// cumulative mass reaches the target is then gathered (at most kExactCap
+// elements), sorted, and resolved with an f64 prefix sum.  A bin with more
+// elements is split once more into kBins sub-bins by the fraction of
+// (y0 - y) * mul, which is exact for a non-clamped bin; a sub-bin that is
+// still too big (many equal values) is left to the radix selections.
+struct VBins {
+    float y0, mul;
+    __device__ __forceinline__ float pos(float y) const { return (y0 - y) * mul; }
+    __device__ __forceinline__ uint32_t bin(float y) const {
+        const float d = pos(y);
+        return d >= static_cast<float>(kBins - 1) ? kBins - 1u : (d > 0.0f ? static_cast<uint32_t>(d) : 0u);
+    }
+    // level-2 index of y inside bin b < kBins - 1, where pos(y) - b in [0, 1) is exact
+    __device__ __forceinline__ uint32_t sub(float y, uint32_t b) const {
+        const float fr = (pos(y) - static_cast<float>(b)) * static_cast<float>(kBins);
+        return fr >= static_cast<float>(kBins - 1) ? kBins - 1u : (fr > 0.0f ? static_cast<uint32_t>(fr) : 0u);
+    }
+};
+static_assert(kBins == 2 * kBlock, "two bins per thread");
+
+// Counts and f64 masses of the filtered elements per bin (level 1), or per
+// sub-bin of bin b1 (level 2).  Returns false when a filtered value is NaN.
+__device__ __noinline__ bool vbin_hist(Fin& f_in, const Filt& q_in, const VBins& vb_in, bool level2, uint32_t b1) {
+    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
+    const Filt q = q_in;
+    const VBins vb = vb_in;
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t i = tid; i < kBins; i += kBlock) {
+        f.hcnt()[i] = 0;
+        f.hmass()[i] = 0.0;
+    }
+    if (tid == 0) f.misc()[M_VBAD] = 0;
+    TSM_LDS_SYNC();
+    const float t = f.m.t;
+    uint32_t bad = 0;
+    row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
+        const uint64_t c = comp_of(q.order, id, x, y);
+        if (!keep_el(f, q, id, y, c)) return;
+        uint32_t b = vb.bin(y);
+        if (level2) {
+            if (b != b1) return;
+            b = vb.sub(y, b1);
+        }
+        bad |= y != y;
+        atomicAdd(&f.hcnt()[b], 1u);
+        atomicAdd(&f.hmass()[b], static_cast<double>(glibc_expf((y - vb.y0) / t)));
+    });
+    if (bad) f.misc()[M_VBAD] = 1u;
+    TSM_LDS_SYNC();
+    const bool ok = f.misc()[M_VBAD] == 0;
+    TSM_LDS_SYNC();
+    return ok;
+}
+
+// Element count and f64 mass of the histogram.
+__device__ __forceinline__ uint32_t vbin_totals(Fin& f, double* mass) {
+    const uint32_t b0 = 2 * threadIdx.x;
+    block_excl_scan_f64(f.hmass()[b0] + f.hmass()[b0 + 1], f.miscd() + 8, mass);
+    return block_sum<kBlock>(f.hcnt()[b0] + f.hcnt()[b0 + 1], f.tmp());
+}
+
+struct BinHit {
+    uint32_t bin;       // kBins: the histogram is empty
+    uint32_t cnt;       // elements in the bin
+    uint32_t before_n;  // elements in earlier bins
+    double before;      // base + the mass of earlier bins
+};
+
+// The first non-empty bin whose cumulative mass (from base) reaches target,
+// or the last non-empty bin when none does.
+__device__ __forceinline__ BinHit vbin_find(Fin& f, double base, double target) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t b0 = 2 * tid;
+    const uint32_t c0 = f.hcnt()[b0], c1 = f.hcnt()[b0 + 1];
+    const double m0 = f.hmass()[b0], m1 = f.hmass()[b0 + 1];
+    if (tid == 0) {
+        f.misc()[M_FIND] = 0xFFFFFFFFu;
+        f.misc()[M_FIND2] = 0;
+    }
+    double mtot;
+    const double mb = block_excl_scan_f64(m0 + m1, f.miscd() + 8, &mtot);  // barriers order the init above
+    uint32_t ctot;
+    const uint32_t cb = block_excl_scan<kBlock>(c0 + c1, f.tmp(), &ctot);
+    const double bs = base + mb;
+    uint32_t cand = 0xFFFFFFFFu;
+    if (c0 > 0 && bs + m0 >= target) cand = b0;
+    else if (c1 > 0 && bs + m0 + m1 >= target) cand = b0 + 1;
+    if (cand != 0xFFFFFFFFu) atomicMin(&f.misc()[M_FIND], cand);
+    if (c0 + c1 > 0) atomicMax(&f.misc()[M_FIND2], (c1 > 0 ? b0 + 1 : b0) + 1);
+    TSM_LDS_SYNC();
+    uint32_t d = f.misc()[M_FIND];
+    if (d == 0xFFFFFFFFu) d = f.misc()[M_FIND2] == 0 ? kBins : f.misc()[M_FIND2] - 1;
+    if (d < kBins && (d >> 1) == tid) {
+        const bool second = d & 1u;
+        f.miscd()[0] = bs + (second ? m0 : 0.0);
+        f.misc()[M_CNT] = cb + (second ? c0 : 0u);
+        f.misc()[M_TOTAL] = second ? c1 : c0;
+    }
+    TSM_LDS_SYNC();
+    BinHit h;
+    h.bin = d;
+    h.cnt = d < kBins ? f.misc()[M_TOTAL] : 0u;
+    h.before_n = d < kBins ? f.misc()[M_CNT] : ctot;
+    h.before = d < kBins ? f.miscd()[0] : base + mtot;
+    TSM_LDS_SYNC();
+    return h;
+}
+
+// Gathers the filtered elements of bin b1 (level 1) or of its sub-bin b2
+// (level 2), sorts them, and returns the first whose cumulative mass (from
+// h.before) reaches target, or the last.  False when the bin holds more than
+// kExactCap elements.
+__device__ __forceinline__ bool vbin_resolve(Fin& f, const Filt& q, const VBins& vb, bool level2, uint32_t b1, const BinHit& h,
+                             uint32_t before_n, double target, MassSel* out) {
+    const uint32_t tid = threadIdx.x;
+    if (h.bin >= kBins || h.cnt == 0 || h.cnt > kExactCap) return false;
+    const uint32_t b2 = h.bin;
+    if (tid == 0) f.misc()[M_CNT] = 0;
+    TSM_LDS_SYNC();
+    row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
+        const uint64_t c = comp_of(q.order, id, x, y);
+        if (!keep_el(f, q, id, y, c)) return;
+        const uint32_t b = vb.bin(y);
+        if (b != b1 || (level2 && vb.sub(y, b1) != b2)) return;
+        const uint32_t pos = atomicAdd(&f.misc()[M_CNT], 1u);
+        if (pos < kExactCap) f.gcomp()[pos] = c;
+    });
+    const uint32_t n = min(f.misc()[M_CNT], kExactCap);
+    TSM_LDS_SYNC();
+    if (n == 0) return false;
+    sort_u64(f.gcomp(), n);
+    TSM_LDS_SYNC();
+    double p = 0.0;
+    uint64_t c = 0;
+    if (tid < n) {
+        c = f.gcomp()[tid];
+        const float y = key_to_float(~static_cast<uint32_t>(c >> 32));
+        p = static_cast<double>(glibc_expf((y - vb.y0) / f.m.t));
+    }
+    if (tid == 0) f.misc()[M_FIND] = 0xFFFFFFFFu;
+    double tot;
+    const double incl = h.before + (block_excl_scan_f64(p, f.miscd() + 8, &tot) + p);
+    if (tid < n && incl >= target) atomicMin(&f.misc()[M_FIND], tid);
+    TSM_LDS_SYNC();
+    uint32_t j = f.misc()[M_FIND];
+    if (j == 0xFFFFFFFFu) j = n - 1;
+    if (tid == j) {
+        f.miscd()[0] = incl;
+        f.gcomp()[kExactCap - 1] = c;  // sorted list no longer needed
+    }
+    TSM_LDS_SYNC();
+    out->T = f.gcomp()[kExactCap - 1];
+    out->cum = f.miscd()[0];
+    out->rank = before_n + j + 1;
+    TSM_LDS_SYNC();
+    return true;
+}
+
+// mass selection over the histogram in LDS (level 1 bins of q): the element
+// of q whose cumulative mass reaches target.  *l1 is cleared when the level-1
+// histogram was overwritten.  False when the radix selection must decide.
+__device__ __noinline__ bool vbin_select(Fin& f_in, const Filt& q_in, const VBins& vb_in, double target, MassSel* out,
+                                         BinHit* hit, bool* l1) {
+    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
+    const Filt q = q_in;
+    const VBins vb = vb_in;
+    const BinHit h = vbin_find(f, 0.0, target);
+    *hit = h;
+    if (h.bin >= kBins) return false;
+    if (h.cnt <= kExactCap) return vbin_resolve(f, q, vb, false, h.bin, h, h.before_n, target, out);
+    if (h.bin >= kBins - 1) return false;  // clamped bin: no exact split
+    *l1 = false;
+    if (!vbin_hist(f, q, vb, true, h.bin)) return false;
+    const BinHit h2 = vbin_find(f, h.before, target);
+    return vbin_resolve(f, q, vb, true, h.bin, h2, h.before_n + h2.before_n, target, out);
 }
 
 struct Pick {
@@ -640,51 +850,181 @@ __device__ uint32_t reread_topk_list(Fin& f, uint32_t nallow) {
     return len;
 }
 
+// Top-p and the draw from one gather.  The kept mass M lies in (before,
+// before + mass] of the top-p bin hp, so the draw target u * M can only fall
+// in the bins that cover [u * before, u * (before + mass)]: hp and those bins
+// are gathered together, sorted, and both picks are resolved from the list
+// with f64 prefix sums.  False (nothing decided, the histogram intact) when
+// they hold more than kExactCap elements; the caller then selects in passes
+// of their own.
+__device__ __noinline__ bool vbin_topp_draw(Fin& f_in, const Filt& q_in, const VBins& vb_in, double target_p,
+                                            float u, MassSel* sp, uint64_t* drawn) {
+    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
+    const Filt q = q_in;
+    const VBins vb = vb_in;
+    const uint32_t tid = threadIdx.x;
+    const BinHit hp = vbin_find(f, 0.0, target_p);
+    if (hp.bin >= kBins || hp.cnt == 0 || hp.cnt > kExactCap) return false;
+    const double hmass_p = f.hmass()[hp.bin];
+    const double du = static_cast<double>(u);
+    const BinHit hlo = vbin_find(f, 0.0, du * hp.before);
+    const BinHit hhi = vbin_find(f, 0.0, du * (hp.before + hmass_p));
+    const uint32_t jlo = min(hlo.bin, hp.bin), jhi = min(hhi.bin, hp.bin);
+    // bins jlo..jhi (contiguous) and hp.bin; hp's elements sort last
+    const uint32_t n_low = jhi < hp.bin ? (hhi.before_n + hhi.cnt) - hlo.before_n : hp.before_n - hlo.before_n;
+    const uint32_t want_n = n_low + hp.cnt;
+    if (want_n > kExactCap) return false;
+    if (tid == 0) f.misc()[M_CNT] = 0;
+    TSM_LDS_SYNC();
+    const uint32_t bstar = hp.bin;
+    row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
+        const uint64_t c = comp_of(q.order, id, x, y);
+        if (!keep_el(f, q, id, y, c)) return;
+        const uint32_t b = vb.bin(y);
+        if (b != bstar && (b < jlo || b > jhi)) return;
+        const uint32_t pos = atomicAdd(&f.misc()[M_CNT], 1u);
+        if (pos < kExactCap) f.gcomp()[pos] = c;
+    });
+    const uint32_t n = f.misc()[M_CNT];
+    TSM_LDS_SYNC();
+    if (n != want_n) return false;  // not reached: the histogram counted the same elements
+    sort_u64(f.gcomp(), n);
+    TSM_LDS_SYNC();
+    const uint32_t s0 = n - hp.cnt;  // list index of hp's first element
+    double p = 0.0;
+    uint64_t c = 0;
+    if (tid < n) {
+        c = f.gcomp()[tid];
+        const float y = key_to_float(~static_cast<uint32_t>(c >> 32));
+        p = static_cast<double>(glibc_expf((y - vb.y0) / f.m.t));
+    }
+    // top-p inside hp
+    if (tid == 0) {
+        f.misc()[M_FIND] = 0xFFFFFFFFu;
+        f.misc()[M_FIND2] = 0xFFFFFFFFu;
+    }
+    double tot;
+    const double pin = tid >= s0 ? p : 0.0;
+    const double cum_p = hp.before + (block_excl_scan_f64(pin, f.miscd() + 8, &tot) + pin);
+    if (tid >= s0 && tid < n && cum_p >= target_p) atomicMin(&f.misc()[M_FIND], tid);
+    TSM_LDS_SYNC();
+    uint32_t jp = f.misc()[M_FIND];
+    if (jp == 0xFFFFFFFFu) jp = n - 1;
+    if (tid == jp) f.miscd()[0] = cum_p;
+    TSM_LDS_SYNC();
+    const double M = f.miscd()[0];
+    const double td = du * M;
+    // the draw: inside hp (through the top-p pick) or in bins jlo..jhi; with
+    // no bin gathered below hp, hp holds the row's first elements
+    const bool in_hp = td > hp.before || s0 == 0;
+    const double plo = (!in_hp && tid < s0) ? p : 0.0;
+    const double cum_d = in_hp ? cum_p : hlo.before + (block_excl_scan_f64(plo, f.miscd() + 8, &tot) + plo);
+    const uint32_t lo_j = in_hp ? s0 : 0u, hi_j = in_hp ? jp + 1 : s0;
+    if (tid >= lo_j && tid < hi_j && cum_d >= td) atomicMin(&f.misc()[M_FIND2], tid);
+    TSM_LDS_SYNC();
+    uint32_t jd = f.misc()[M_FIND2];
+    bool ok = true;
+    if (jd == 0xFFFFFFFFu) {
+        if (in_hp) jd = jp;  // u * M reaches past the pick only by rounding: the last kept
+        else ok = false;     // rounding put the target outside the gathered bins
+    }
+    TSM_LDS_SYNC();
+    if (!ok) return false;
+    sp->T = f.gcomp()[jp];
+    sp->cum = M;
+    sp->rank = hp.before_n + (jp - s0) + 1;
+    *drawn = f.gcomp()[jd];
+    TSM_LDS_SYNC();
+    return true;
+}
+
+// Restricts the level-1 histogram to the elements through the top-p pick,
+// which lies in bin hb: later bins are emptied and bin hb keeps its kept part.
+__device__ __forceinline__ void vbin_cut(Fin& f, const BinHit& hb, uint32_t keep, double mass) {
+    for (uint32_t i = threadIdx.x; i < kBins; i += kBlock) {
+        if (i > hb.bin) {
+            f.hcnt()[i] = 0;
+            f.hmass()[i] = 0.0;
+        } else if (i == hb.bin) {
+            f.hcnt()[i] = keep - hb.before_n;
+            f.hmass()[i] = mass - hb.before;
+        }
+    }
+    TSM_LDS_SYNC();
+}
+
+// Up to kExactCap survivors: gathered, sorted and finished exactly.
+__device__ __noinline__ Pick nucleus_exact(Fin& f_in, const Filt& q_in, float u, const DistOut* dist) {
+    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
+    const Filt q = q_in;
+    const uint32_t g = gather_pass(f, q, kExactCap);
+    sort_gathered(f, g);
+    return finish_list(f, g, u, dist);
+}
+
 // Rows without top-k (window > 1024): the cutoff set (sampler.rs:195-208),
 // the window rule, truncation to want, min-p, then top-p and the draw, all
 // by re-reading the row.  Up to 1024 survivors are finished exactly
-// (finish_list); larger sets use f64 mass selection.
-__device__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* dist) {
+// (finish_list); larger sets use f64 mass selections, through value bins
+// where they resolve and through radix rounds otherwise.
+__device__ __noinline__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* dist) {
     const uint32_t tid = threadIdx.x;
     const RowMode& m = f.m;
-    float mall = -INFINITY, mal = -INFINITY;
+    float mall = -INFINITY, mal = -INFINITY, mlo = INFINITY;
     {
-        float la = -INFINITY, lb = -INFINITY;
-        row_pass(f, [&](uint32_t id, float x, float y) {
+        float la = -INFINITY, lb = -INFINITY, lc = INFINITY;
+        row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
             la = fmaxf(la, y);
+            lc = fminf(lc, y);
             if (m.constrained && allowed_bit(f, id)) lb = fmaxf(lb, y);
         });
         la = wave_max(la);
         lb = wave_max(lb);
+        lc = -wave_max(-lc);
         float* ftmp = reinterpret_cast<float*>(f.miscd() + 8);
         if ((tid & 63) == 0) {
             ftmp[tid / 64] = la;
             ftmp[16 + tid / 64] = lb;
+            ftmp[32 + tid / 64] = lc;
         }
         TSM_LDS_SYNC();
         for (int w = 0; w < kBlock / kWave; w++) {
             mall = fmaxf(mall, ftmp[w]);
             mal = fmaxf(mal, ftmp[16 + w]);
+            mlo = fminf(mlo, ftmp[32 + w]);
         }
         TSM_LDS_SYNC();
     }
     const float cut = mall - 30.0f * m.t;  // sampler.rs:198-199
+    const float y0 = m.constrained ? mal : mall;
+    // value bins over [y0 - 30.5 t, y0], or the row's narrower range
+    VBins vb;
+    vb.y0 = y0;
+    {
+        float span = fminf(30.5f, (y0 - mlo) / m.t);
+        if (!(span > 0.0f)) span = 1.0f;
+        vb.mul = (static_cast<float>(kBins) / span) / m.t;
+    }
+    bool use_vb = m.t > 0.0f && __builtin_isfinite(y0) && __builtin_isfinite(vb.mul) && vb.mul > 0.0f;
+    bool hist_ok = false;  // the level-1 histogram in LDS is that of q2
     Filt q0;
     q0.order = ORD_TOTAL_Y;
     q0.use_cut = true;
     q0.cut = cut;
-    float y0 = mall;
+    q0.need_allowed = m.constrained;
     uint32_t n0;
-    if (m.constrained) {
-        q0.need_allowed = true;
-        n0 = count_pass(f, q0);
-        if (n0 == 0) {  // sampler.rs:211-221
-            q0.use_cut = false;
-            n0 = nallow;
-        }
-        y0 = mal;
+    if (use_vb) {
+        use_vb = vbin_hist(f, q0, vb, false, 0);
+        double mass0;
+        n0 = vbin_totals(f, &mass0);
+        hist_ok = use_vb;
     } else {
         n0 = count_pass(f, q0);
+    }
+    if (m.constrained && n0 == 0) {  // sampler.rs:211-221
+        q0.use_cut = false;
+        n0 = nallow;
+        hist_ok = false;
     }
     Filt q1 = q0;
     uint32_t n1 = n0;
@@ -692,6 +1032,7 @@ __device__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* 
         q1.use_max = true;
         q1.max_comp = select_kth(f, q0, m.want);
         n1 = m.want;
+        hist_ok = false;
     }
     Filt q2 = q1;
     uint32_t n2c = n1;
@@ -706,19 +1047,44 @@ __device__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* 
             q2.max_comp = select_kth(f, q1, 1);
             n2c = 1;
         }
+        hist_ok = false;
     }
-    if (n2c <= kExactCap) {
-        const uint32_t g = gather_pass(f, q2, kExactCap);
-        sort_gathered(f, g);
-        return finish_list(f, g, u, dist);
-    }
+    if (n2c <= kExactCap) return nucleus_exact(f, q2, u, dist);
     // more than 1024 candidates: exact-arithmetic (f64) cumulative sums
-    const double total = mass_total(f, q2, y0);
+    double total;
+    if (use_vb && !hist_ok) {
+        use_vb = vbin_hist(f, q2, vb, false, 0);
+        hist_ok = use_vb;
+    }
+    if (hist_ok) vbin_totals(f, &total);
+    else total = mass_total(f, q2, y0);
     Filt q3 = q2;
     double mass = total;
     uint32_t keep = n2c;
+    BinHit hp;
+    hp.bin = kBins;
+    if (!(f.P.top_p >= 1.0f) && !dist && hist_ok) {
+        // top-p and the draw from one gather
+        const double target = static_cast<double>(f.P.top_p) * total;
+        MassSel sp;
+        uint64_t ce;
+        if (vbin_topp_draw(f, q2, vb, target, u, &sp, &ce)) {
+            Pick pk;
+            pk.keep = sp.rank;
+            pk.mass = static_cast<float>(sp.cum);
+            const float yk = key_to_float(~static_cast<uint32_t>(ce >> 32));
+            pk.token = static_cast<uint32_t>(ce);
+            pk.prob = static_cast<float>(static_cast<double>(glibc_expf((yk - y0) / m.t)) / sp.cum);
+            return pk;
+        }
+    }
     if (!(f.P.top_p >= 1.0f)) {
-        const MassSel sp = mass_select(f, q2, y0, static_cast<double>(f.P.top_p) * total);
+        const double target = static_cast<double>(f.P.top_p) * total;
+        MassSel sp;
+        if (!(hist_ok && vbin_select(f, q2, vb, target, &sp, &hp, &hist_ok))) {
+            hist_ok = false;
+            sp = mass_select(f, q2, y0, target);
+        }
         q3.use_max = true;
         q3.max_comp = sp.T;
         mass = sp.cum;
@@ -746,8 +1112,25 @@ __device__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* 
         TSM_LDS_SYNC();
         return pk;
     }
-    const MassSel sr = mass_select(f, q3, y0, static_cast<double>(u) * mass);
-    const uint64_t ce = exact_at(f, q3, sr.T);
+    // the draw among the kept (sampler.rs:142-150)
+    const double dtarget = static_cast<double>(u) * mass;
+    uint64_t ce;
+    bool drawn = false;
+    if (use_vb) {
+        if (hist_ok && hp.bin < kBins) vbin_cut(f, hp, keep, mass);
+        if (!hist_ok) hist_ok = vbin_hist(f, q3, vb, false, 0);
+        MassSel sd;
+        BinHit hd;
+        bool l1 = true;
+        if (hist_ok && vbin_select(f, q3, vb, dtarget, &sd, &hd, &l1)) {
+            ce = sd.T;
+            drawn = true;
+        }
+    }
+    if (!drawn) {
+        const MassSel sr = mass_select(f, q3, y0, dtarget);
+        ce = exact_at(f, q3, sr.T);
+    }
     const float yk = key_to_float(~static_cast<uint32_t>(ce >> 32));
     pk.token = static_cast<uint32_t>(ce);
     pk.prob = static_cast<float>(static_cast<double>(glibc_expf((yk - y0) / m.t)) / mass);

@@ -229,9 +229,11 @@ CONFIGS = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5}
 
 
 def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, mask_frac=0.3,
-                logprobs=True, hist_len=16, penalties=True, mode="mixed", sigma=2.0):
+                logprobs=True, hist_len=16, penalties=True, mode="mixed", sigma=2.0, outlier=None):
     """Small random workload for parity tests: mixed per-row settings, optional
-    heavy ties (integer-valued logits), masks and histories."""
+    heavy ties (integer-valued logits), masks and histories.  `outlier` sets
+    id 0 of every row to that value (a narrow cluster of logits next to one
+    far value)."""
     rng = np.random.default_rng(seed)
     stride = stride or vocab
     if ties:
@@ -239,6 +241,8 @@ def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, 
         x[rng.random((rows, stride)) < 0.05] = -0.0
     else:
         x = (rng.standard_normal((rows, stride)) * sigma).astype(np.float32)
+    if outlier is not None:
+        x[:, 0] = np.float32(outlier)
     p = make_params(rows)
     for r in range(rows):
         kind = mode if mode != "mixed" else ["greedy", "topk", "topp", "nucleus", "minp", "all"][r % 6]

@@ -42,6 +42,7 @@
 #define __builtin_amdgcn_update_dpp(old, src, ctrl, rm, bm, bc) emu_dpp((old), (src), (ctrl), (rm), (bm), (bc))
 #define __builtin_amdgcn_wave_barrier() ::emu::wave_sync()
 #define HIP_SYMBOL(x) (&(x))
+#define TSM_GLOBAL_AS
 #define TSM_CONST_AS  // the host has one address space
 
 struct dim3 {

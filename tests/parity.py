@@ -102,6 +102,11 @@ RANDOM_CASES = [
     dict(seed=13, vocab=20001, rows=18, stride=20003, masked=True),
     dict(seed=14, vocab=70000, rows=12, mode="nucleus", sigma=1.0),
     dict(seed=15, vocab=70000, rows=12, mode="all", masked=True, mask_frac=0.002),
+    # nucleus sets of thousands: equal values beyond one bin's capacity, and a
+    # narrow cluster beside a far outlier (value bins split a second time)
+    dict(seed=16, vocab=15000, rows=6, mode="nucleus", ties=True),
+    dict(seed=17, vocab=15000, rows=6, mode="nucleus", sigma=0.01, outlier=-1.0e4),
+    dict(seed=18, vocab=60000, rows=12, mode="nucleus", sigma=0.003, outlier=-50.0, masked=True, mask_frac=0.5),
 ]
 
 DIST_CASES = [(21, dict(vocab=500, mode="mixed")), (22, dict(vocab=3000, mode="minp")),
