@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <type_traits>
@@ -65,6 +66,30 @@ uint32_t draw(Sampler& s, const std::vector<std::pair<uint32_t, float>>& weighte
         if (r <= 0.0f) return w.first;
     }
     return weighted.empty() ? 0u : weighted.back().first;
+}
+
+namespace {
+float prob_of(const Dist& d, uint32_t t) {
+    for (const auto& e : d)
+        if (e.first == t) return e.second;
+    return 0.0f;
+}
+}  // namespace
+
+Verdict verify(const Dist& p, const Dist& q, uint32_t x, float u) {
+    auto q_of = [&](uint32_t t) { return q.empty() ? (t == x ? 1.0f : 0.0f) : prob_of(q, t); };
+    Verdict v;
+    const float qx = q_of(x);
+    if (qx > 0.0f && u < std::min(prob_of(p, x) / qx, 1.0f)) {
+        v.accept = true;
+        return v;
+    }
+    for (const auto& e : p) {
+        const float r = std::max(e.second - q_of(e.first), 0.0f);
+        if (r > 0.0f) v.resample.emplace_back(e.first, r);
+    }
+    if (v.resample.empty()) v.resample = p;
+    return v;
 }
 
 // Device inputs/outputs and their pinned host mirrors, sized at creation.

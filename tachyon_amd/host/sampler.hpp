@@ -72,6 +72,20 @@ class Sampler {
 // one; the sequential f32 sums of the reference.
 uint32_t draw(Sampler& s, const std::vector<std::pair<uint32_t, float>>& weighted);
 
+// A distribution as (token, p) pairs (speculative.rs: `Dist`).
+using Dist = std::vector<std::pair<uint32_t, float>>;
+
+// The speculative sampling rule (speculative.rs:306-318) for one draft x
+// drawn from q (an empty q: the draft was chosen deterministically), given the
+// target's p, e.g. from BatchSampler::distribution, and a uniform u in [0, 1):
+// accept when q(x) > 0 and u < min(p(x) / q(x), 1); otherwise the replacement
+// is drawn from the residual max(p - q, 0) (p itself when that is empty).
+struct Verdict {
+    bool accept = false;
+    Dist resample;  // when rejected: the distribution to draw the replacement from
+};
+Verdict verify(const Dist& p, const Dist& q, uint32_t x, float u);
+
 // TokenLogprob (sampler.rs:287-295): the pick's log-probability under the raw
 // logits and the best alternatives, best first.
 struct TokenLogprob {

@@ -167,6 +167,35 @@ void greedy_settings() {
     EXPECT(d.temperature == 0.7f && d.top_k == 20 && d.top_p == 0.8f && d.repetition_penalty == 1.05f, "default()");
 }
 
+// ---- speculative sampling (the reference's tests, speculative.rs:349-385) ----
+
+void speculative_sampling_preserves_the_target_distribution() {
+    const Dist p = {{0, 0.5f}, {1, 0.3f}, {2, 0.2f}};
+    const Dist q = {{0, 0.2f}, {1, 0.6f}, {2, 0.2f}};
+    Sampler rng(cfg(1.0f, 0, 1.0f, 1.0f, 7));
+    const int trials = 200000;
+    int counts[3] = {0, 0, 0};
+    for (int i = 0; i < trials; i++) {
+        const uint32_t x = draw(rng, q);
+        const float u = rng.uniform();
+        const Verdict v = verify(p, q, x, u);
+        const uint32_t t = v.accept ? x : draw(rng, v.resample);
+        counts[t]++;
+    }
+    for (int i = 0; i < 3; i++) {
+        const float got = static_cast<float>(counts[i]) / trials;
+        EXPECT(std::fabs(got - p[i].second) < 0.01f, "token %d: %.4f vs %.4f", i, got, p[i].second);
+    }
+}
+
+void deterministic_drafts_reduce_to_greedy() {
+    const Dist p = {{4, 1.0f}};
+    EXPECT(verify(p, {}, 4, 0.99f).accept, "accept");
+    const Verdict v = verify(p, {}, 5, 0.0f);
+    EXPECT(!v.accept && v.resample.size() == 1 && v.resample[0].first == 4 && v.resample[0].second == 1.0f,
+           "resample");
+}
+
 // ---- GPU (the reference's tests, sampler.rs:328-395, through the batched path) ----
 
 void greedy_and_top_k(BatchSampler& bs) {
@@ -326,6 +355,9 @@ int main(int argc, char** argv) {
     run("rng_matches_the_oracle", rng_matches_the_oracle);
     run("draw_matches_the_oracle", draw_matches_the_oracle);
     run("greedy_settings", greedy_settings);
+    run("speculative_sampling_preserves_the_target_distribution",
+        speculative_sampling_preserves_the_target_distribution);
+    run("deterministic_drafts_reduce_to_greedy", deterministic_drafts_reduce_to_greedy);
     if (!cpu_only) {
         BatchSampler bs(0, 16, 8192, 128);
         run("greedy_and_top_k", [&] { greedy_and_top_k(bs); });
