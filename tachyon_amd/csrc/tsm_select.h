@@ -511,7 +511,11 @@ __device__ __noinline__ bool vbin_hist(Fin& f_in, const Filt& q_in, const VBins&
     }
     if (tid == 0) f.misc()[M_VBAD] = 0;
     TSM_LDS_SYNC();
-    const float t = f.m.t;
+    // bin masses locate a target's bin and give the mass before it; they use
+    // the hardware exp2 (relative error of a term below 3e-6, largest for the
+    // smallest terms), while the elements of the bin that is resolved are
+    // summed from exact glibc_expf terms
+    const float l2t = 1.4426950408889634f / f.m.t;
     uint32_t bad = 0;
     row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
         const uint64_t c = comp_of(q.order, id, x, y);
@@ -523,7 +527,7 @@ __device__ __noinline__ bool vbin_hist(Fin& f_in, const Filt& q_in, const VBins&
         }
         bad |= y != y;
         atomicAdd(&f.hcnt()[b], 1u);
-        atomicAdd(&f.hmass()[b], static_cast<double>(glibc_expf((y - vb.y0) / t)));
+        atomicAdd(&f.hmass()[b], static_cast<double>(__builtin_amdgcn_exp2f((y - vb.y0) * l2t)));
     });
     if (bad) f.misc()[M_VBAD] = 1u;
     TSM_LDS_SYNC();
