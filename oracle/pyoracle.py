@@ -48,6 +48,9 @@ class OrRowDiag(ctypes.Structure):
         ("mass64", ctypes.c_double),
         ("mass", ctypes.c_float),
         ("best", ctypes.c_float),
+        ("token_exact", ctypes.c_uint32),
+        ("ugap_exact", ctypes.c_double),
+        ("pgap_exact", ctypes.c_double),
     ]
 
 
@@ -57,6 +60,7 @@ DIAG_DTYPE = np.dtype(
         ("keep_exact", "<u4"), ("pick", "<u4"), ("pick_exact", "<u4"),
         ("consumed_u", "<u4"), ("u_gap", "<f8"), ("p_gap", "<f8"),
         ("mass64", "<f8"), ("mass", "<f4"), ("best", "<f4"),
+        ("token_exact", "<u4"), ("ugap_exact", "<f8"), ("pgap_exact", "<f8"),
     ],
     align=True,
 )

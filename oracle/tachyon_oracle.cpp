@@ -330,6 +330,31 @@ void exact_view(const or_config& cfg, const Scratch& s, size_t len, size_t keep,
         if (keep != keep_exact) d->p_gap = 0.0;
     }
     d->keep_exact = static_cast<uint32_t>(keep_exact);
+    // exact arithmetic throughout: the draw over the mass of keep_exact
+    d->token_exact = len > 0 ? s.ri[0] : 0u;
+    d->ugap_exact = 1.0;
+    d->pgap_exact = 1.0;
+    if (!greedy && cfg.top_p < 1.0f && len > 0) {
+        const double total = c[len - 1];
+        const double p = cfg.top_p;
+        double g = std::fabs(c[keep_exact - 1] / total - p);
+        if (keep_exact >= 2) g = std::min(g, std::fabs(c[keep_exact - 2] / total - p));
+        d->pgap_exact = g;
+    }
+    if (drew && keep_exact > 0) {
+        const double m = c[keep_exact - 1];
+        const double target = static_cast<double>(u) * m;
+        size_t pe = keep_exact - 1;
+        for (size_t j = 0; j < keep_exact; j++)
+            if (c[j] >= target) {
+                pe = j;
+                break;
+            }
+        d->token_exact = s.ri[pe];
+        double g = std::fabs(c[pe] - target);
+        if (pe > 0) g = std::min(g, std::fabs(target - c[pe - 1]));
+        d->ugap_exact = g / m;
+    }
     d->u_gap = 1.0;
     d->pick_exact = static_cast<uint32_t>(pick);
     if (drew && keep > 0) {
@@ -367,6 +392,9 @@ uint32_t pick_impl(const or_config& cfg, Scratch& s, const float* logits, size_t
             d->consumed_u = 0;
             d->u_gap = 1.0;
             d->p_gap = 1.0;
+            d->ugap_exact = 1.0;
+            d->pgap_exact = 1.0;
+            d->token_exact = or_argmax(logits, n);
         }
         return or_argmax(logits, n);
     }
@@ -579,7 +607,8 @@ int or_sample_batch(const float* logits, uint32_t rows, uint32_t row_stride, uin
             pr = 1.0f;
             dl.path = OR_PATH_ARGMAX_FAST;
             dl.ranked = dl.survivors = dl.keep = dl.keep_exact = 1;
-            dl.u_gap = dl.p_gap = 1.0;
+            dl.u_gap = dl.p_gap = dl.ugap_exact = dl.pgap_exact = 1.0;
+            dl.token_exact = tok;
         } else {
             tok = pick_impl(cfg, s, x, n, recent, nrecent, mrow, uniforms[r], &kp, &pr, &dl);
         }

@@ -59,6 +59,12 @@ typedef struct or_row_diag {
     double   mass64;     /* exact sum of the kept probabilities              */
     float    mass;       /* the reference's f32 mass                          */
     float    best;       /* ranked[0] penalized logit (l0)                   */
+    uint32_t token_exact; /* the pick with exact (f64) sums throughout: top-p
+                             keeps keep_exact, the draw spans their mass      */
+    double   ugap_exact; /* distance of u * mass from the CDF boundaries of
+                            that pick, relative to its mass (1 if no draw)   */
+    double   pgap_exact; /* distance of top_p from the exact cumulatives at
+                            keep_exact - 1 and keep_exact (1 if top-p off)    */
 } or_row_diag;
 
 /* ---- building blocks, each a restatement of one reference function ---- */
