@@ -86,6 +86,9 @@ struct Filt {
     uint64_t max_comp = ~0ull;
     float y0 = 0.0f;
     float minp = 0.0f;
+    // min-p band: y >= minp_hi is kept and y < minp_lo dropped without the
+    // exponential; only values in between evaluate it
+    float minp_lo = 0.0f, minp_hi = 0.0f;
 };
 
 // One row being finished: its global inputs and settings.  LDS structures are
@@ -135,7 +138,10 @@ __device__ __forceinline__ bool keep_el(const Fin& f, const Filt& q, uint32_t id
     if (q.need_allowed && !allowed_bit(f, id)) return false;
     if (q.use_cut && !(y >= q.cut)) return false;
     if (q.use_max && c > q.max_comp) return false;
-    if (q.use_minp && !(glibc_expf((y - q.y0) / f.m.t) >= q.minp)) return false;
+    if (q.use_minp) {
+        if (y < q.minp_lo) return false;
+        if (!(y >= q.minp_hi) && !(glibc_expf((y - q.y0) / f.m.t) >= q.minp)) return false;
+    }
     return true;
 }
 
@@ -1044,6 +1050,14 @@ __device__ __noinline__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, co
         q2.use_minp = true;
         q2.y0 = y0;
         q2.minp = f.P.min_p;
+        // p >= min_p  <=>  y >= y0 + t ln(min_p), up to the roundings of the
+        // subtraction, the division and expf (below 1e-6 relative): a band of
+        // 1e-3 (|y0| + |t ln min_p| + t) on either side holds every value
+        // those roundings could put on the other side
+        const float a = m.t * logf(f.P.min_p);
+        const float band = 1e-3f * (fabsf(y0) + fabsf(a) + m.t);
+        q2.minp_lo = (y0 + a) - band;
+        q2.minp_hi = (y0 + a) + band;
         n2c = count_pass(f, q2);
         if (n2c == 0) {
             q2 = q1;
