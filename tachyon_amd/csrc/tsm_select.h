@@ -220,9 +220,10 @@ __device__ __forceinline__ uint32_t pow2_ceil(uint32_t v) {
 }
 
 // Counts filtered elements (one pass).
+template <int G = 1>
 __device__ __forceinline__ uint32_t count_pass(Fin& f, const Filt& q) {
     uint32_t local = 0;
-    row_pass(f, [&](uint32_t id, float x, float y) {
+    row_pass<G>(f, [&](uint32_t id, float x, float y) {
         const uint64_t c = comp_of(q.order, id, x, y);
         if (keep_el(f, q, id, y, c)) local++;
     });
@@ -422,10 +423,11 @@ __device__ __forceinline__ double mass_total(Fin& f, const Filt& q, float y0) {
 }
 
 // Gathers filtered elements' composites into gcomp (caller guarantees <= cap).
+template <int G = 1>
 __device__ __forceinline__ uint32_t gather_pass(Fin& f, const Filt& q, uint32_t cap) {
     if (threadIdx.x == 0) f.misc()[M_CNT] = 0;
     TSM_LDS_SYNC();
-    row_pass(f, [&](uint32_t id, float x, float y) {
+    row_pass<G>(f, [&](uint32_t id, float x, float y) {
         const uint64_t c = comp_of(q.order, id, x, y);
         if (keep_el(f, q, id, y, c)) {
             const uint32_t pos = atomicAdd(&f.misc()[M_CNT], 1u);
@@ -967,7 +969,7 @@ __device__ __forceinline__ void vbin_cut(Fin& f, const BinHit& hb, uint32_t keep
 __device__ __noinline__ Pick nucleus_exact(Fin& f_in, const Filt& q_in, float u, const DistOut* dist) {
     Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
     const Filt q = q_in;
-    const uint32_t g = gather_pass(f, q, kExactCap);
+    const uint32_t g = gather_pass<kNucGroup>(f, q, kExactCap);
     sort_gathered(f, g);
     return finish_list(f, g, u, dist);
 }
@@ -1023,13 +1025,17 @@ __device__ __noinline__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, co
     q0.cut = cut;
     q0.need_allowed = m.constrained;
     uint32_t n0;
-    if (use_vb) {
+    if (f.P.min_p > 0.0f && !m.constrained && m.want >= f.n) {
+        // the cutoff set's size decides nothing here (no truncation, no
+        // fallback): min-p's count below is the first one needed
+        n0 = m.want;
+    } else if (use_vb) {
         use_vb = vbin_hist(f, q0, vb, false, 0);
         double mass0;
         n0 = vbin_totals(f, &mass0);
         hist_ok = use_vb;
     } else {
-        n0 = count_pass(f, q0);
+        n0 = count_pass<kNucGroup>(f, q0);
     }
     if (m.constrained && n0 == 0) {  // sampler.rs:211-221
         q0.use_cut = false;
@@ -1058,7 +1064,7 @@ __device__ __noinline__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, co
         const float band = 1e-3f * (fabsf(y0) + fabsf(a) + m.t);
         q2.minp_lo = (y0 + a) - band;
         q2.minp_hi = (y0 + a) + band;
-        n2c = count_pass(f, q2);
+        n2c = count_pass<kNucGroup>(f, q2);
         if (n2c == 0) {
             q2 = q1;
             q2.use_max = true;
