@@ -477,6 +477,22 @@ __device__ void sort_gathered(Fin& f, uint32_t n) {
     TSM_LDS_SYNC();
 }
 
+// Sorts a[0..n) ascending, n <= kBlock distinct values: each thread ranks
+// its value by counting the smaller ones (broadcast LDS reads, no barrier per
+// stage as in a bitonic sort) and stores it at its rank.
+__device__ __forceinline__ void rank_sort_u64(uint64_t* a, uint32_t n) {
+    const uint32_t tid = threadIdx.x;
+    uint64_t v = 0;
+    uint32_t r = 0;
+    if (tid < n) {
+        v = a[tid];
+        for (uint32_t j = 0; j < n; j++) r += a[j] < v ? 1u : 0u;
+    }
+    TSM_LDS_SYNC();
+    if (tid < n) a[r] = v;
+    TSM_LDS_SYNC();
+}
+
 constexpr int kNucGroup = 4;  // loads in flight per thread in the nucleus passes
 
 // ---- value-binned mass selection -------------------------------------------------
@@ -598,6 +614,55 @@ __device__ __forceinline__ BinHit vbin_find(Fin& f, double base, double target) 
     return h;
 }
 
+// vbin_find for two targets (from base 0) with one scan of the bins.
+__device__ __forceinline__ void vbin_find2(Fin& f, double ta, double tb, BinHit* ha, BinHit* hb) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t b0 = 2 * tid;
+    const uint32_t c0 = f.hcnt()[b0], c1 = f.hcnt()[b0 + 1];
+    const double m0 = f.hmass()[b0], m1 = f.hmass()[b0 + 1];
+    uint32_t* fs = f.misc() + M_RED;  // first hits [0..1], last non-empty + 1 [2], per target: before_n, cnt
+    if (tid == 0) {
+        fs[0] = fs[1] = 0xFFFFFFFFu;
+        fs[2] = 0;
+    }
+    double mtot;
+    const double bs = block_excl_scan_f64(m0 + m1, f.miscd() + 8, &mtot);  // barriers order the init above
+    uint32_t ctot;
+    const uint32_t cb = block_excl_scan<kBlock>(c0 + c1, f.tmp(), &ctot);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const double target = k == 0 ? ta : tb;
+        uint32_t cand = 0xFFFFFFFFu;
+        if (c0 > 0 && bs + m0 >= target) cand = b0;
+        else if (c1 > 0 && bs + m0 + m1 >= target) cand = b0 + 1;
+        if (cand != 0xFFFFFFFFu) atomicMin(&fs[k], cand);
+    }
+    if (c0 + c1 > 0) atomicMax(&fs[2], (c1 > 0 ? b0 + 1 : b0) + 1);
+    TSM_LDS_SYNC();
+    uint32_t d[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        d[k] = fs[k];
+        if (d[k] == 0xFFFFFFFFu) d[k] = fs[2] == 0 ? kBins : fs[2] - 1;
+        if (d[k] < kBins && (d[k] >> 1) == tid) {
+            const bool second = d[k] & 1u;
+            f.miscd()[k] = bs + (second ? m0 : 0.0);
+            fs[3 + k] = cb + (second ? c0 : 0u);
+            fs[5 + k] = second ? c1 : c0;
+        }
+    }
+    TSM_LDS_SYNC();
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        BinHit* h = k == 0 ? ha : hb;
+        h->bin = d[k];
+        h->cnt = d[k] < kBins ? fs[5 + k] : 0u;
+        h->before_n = d[k] < kBins ? fs[3 + k] : ctot;
+        h->before = d[k] < kBins ? f.miscd()[k] : mtot;
+    }
+    TSM_LDS_SYNC();
+}
+
 // Gathers the filtered elements of bin b1 (level 1) or of its sub-bin b2
 // (level 2), sorts them, and returns the first whose cumulative mass (from
 // h.before) reaches target, or the last.  False when the bin holds more than
@@ -620,7 +685,7 @@ __device__ __forceinline__ bool vbin_resolve(Fin& f, const Filt& q, const VBins&
     const uint32_t n = min(f.misc()[M_CNT], kExactCap);
     TSM_LDS_SYNC();
     if (n == 0) return false;
-    sort_u64(f.gcomp(), n);
+    rank_sort_u64(f.gcomp(), n);
     TSM_LDS_SYNC();
     double p = 0.0;
     uint64_t c = 0;
@@ -879,8 +944,8 @@ __device__ __noinline__ bool vbin_topp_draw(Fin& f_in, const Filt& q_in, const V
     if (hp.bin >= kBins || hp.cnt == 0 || hp.cnt > kExactCap) return false;
     const double hmass_p = f.hmass()[hp.bin];
     const double du = static_cast<double>(u);
-    const BinHit hlo = vbin_find(f, 0.0, du * hp.before);
-    const BinHit hhi = vbin_find(f, 0.0, du * (hp.before + hmass_p));
+    BinHit hlo, hhi;
+    vbin_find2(f, du * hp.before, du * (hp.before + hmass_p), &hlo, &hhi);
     const uint32_t jlo = min(hlo.bin, hp.bin), jhi = min(hhi.bin, hp.bin);
     // bins jlo..jhi (contiguous) and hp.bin; hp's elements sort last
     const uint32_t n_low = jhi < hp.bin ? (hhi.before_n + hhi.cnt) - hlo.before_n : hp.before_n - hlo.before_n;
@@ -900,7 +965,7 @@ __device__ __noinline__ bool vbin_topp_draw(Fin& f_in, const Filt& q_in, const V
     const uint32_t n = f.misc()[M_CNT];
     TSM_LDS_SYNC();
     if (n != want_n) return false;  // not reached: the histogram counted the same elements
-    sort_u64(f.gcomp(), n);
+    rank_sort_u64(f.gcomp(), n);
     TSM_LDS_SYNC();
     const uint32_t s0 = n - hp.cnt;  // list index of hp's first element
     double p = 0.0;
