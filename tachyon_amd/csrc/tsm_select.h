@@ -1050,7 +1050,7 @@ __device__ __noinline__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, co
     float mall = -INFINITY, mal = -INFINITY, mlo = INFINITY;
     {
         float la = -INFINITY, lb = -INFINITY, lc = INFINITY;
-        row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
+        row_pass<2 * kNucGroup>(f, [&](uint32_t id, float x, float y) {
             la = fmaxf(la, y);
             lc = fminf(lc, y);
             if (m.constrained && allowed_bit(f, id)) lb = fmaxf(lb, y);
