@@ -87,7 +87,27 @@ typedef struct tsm_batch {
     const uint32_t*       mask;         /* [rows][mask_stride], NULL if no row
                                            sets TSM_ROW_CONSTRAINED             */
     const float*          uniforms;     /* [rows], each in [0, 1)               */
+    uint32_t              row_kinds;    /* OR of tsm_row_kind() over the rows
+                                           (host-side configs), or 0 when not
+                                           known: then every kernel is queued */
+    uint32_t              reserved;     /* must be 0                            */
 } tsm_batch;
+
+/*
+ * Row kinds.  In a batch of up to 16 rows a step queues one kernel per kind
+ * present: the split-row kernel (a row cut over many workgroups) for rows
+ * with a top-k window (sampler.rs:192-194) and a short penalizing history,
+ * the whole-row kernel for the others (no top-k: the 30*T cutoff set,
+ * sampler.rs:195-208; long histories).  Larger batches take the whole-row
+ * kernel for every row.  A batch that names its kinds skips the kernels it
+ * does not need (about 2 us each); in a small batch, a row of a kind the
+ * batch did not name is not sampled and sets TSM_STATUS_ROW_KIND.
+ * tsm_row_kind() gives a row's kind from the same fields the device reads:
+ * its parameters, the batch's `usable`, the row's history length and whether
+ * the batch has a mask.
+ */
+#define TSM_ROWKIND_SPLIT 1u
+#define TSM_ROWKIND_WHOLE 2u
 
 /* One step's outputs.  `token` is required; every other pointer may be NULL. */
 typedef struct tsm_outputs {
@@ -155,7 +175,14 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
 #define TSM_STATUS_DIST_TRUNCATED   4u
 #define TSM_STATUS_INTERNAL         8u /* a selection found no element (e.g. a
                                           row of NaN logits); token 0 written */
+#define TSM_STATUS_ROW_KIND        16u /* a row of a kind the batch's row_kinds
+                                          left out: token 0 written           */
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);
+
+/* The kind (TSM_ROWKIND_*) of a row: `p` is the row's parameters (host
+ * memory), `usable` the batch's, `hist_len` the row's history length,
+ * `has_mask` whether the batch passes a mask. */
+uint32_t tsm_row_kind(const tsm_row_params* p, uint32_t usable, uint32_t hist_len, int has_mask);
 
 /* Library version string, e.g. "tachyon-sampler 0.1 gfx950". */
 const char* tsm_version(void);

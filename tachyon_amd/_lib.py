@@ -28,6 +28,8 @@ class TsmBatch(ctypes.Structure):
         ("hist_offsets", vp),
         ("mask", vp),
         ("uniforms", vp),
+        ("row_kinds", u32),
+        ("reserved", u32),
     ]
 
 
@@ -44,7 +46,10 @@ class TsmOutputs(ctypes.Structure):
     ]
 
 
-SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version"]
+SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version",
+           "tsm_row_kind"]
+ROWKIND_SPLIT = 1
+ROWKIND_WHOLE = 2
 
 _lib = None
 
@@ -75,6 +80,8 @@ def lib():
         L.tsm_status.argtypes = [vp, ctypes.POINTER(u32), ctypes.c_char_p, ctypes.c_size_t]
         L.tsm_version.restype = ctypes.c_char_p
         L.tsm_version.argtypes = []
+        L.tsm_row_kind.restype = u32
+        L.tsm_row_kind.argtypes = [vp, u32, u32, ctypes.c_int]
         _lib = L
     return _lib
 

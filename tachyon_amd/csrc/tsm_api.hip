@@ -5,11 +5,14 @@
 #include <cstring>
 
 #include "tsm_sample.h"
+#include "tsm_split.h"
 
 struct tsm_ctx {
     int device;
     uint32_t max_rows, max_vocab;
     uint32_t* status;  // TSM_STATUS_* bits of the calls since the last tsm_status()
+    void* split_mem;   // the split kernel's scratch (tsm::split::SplitScratch)
+    tsm::split::SplitScratch split;
 };
 
 namespace {
@@ -51,6 +54,9 @@ int check_batch(const tsm_ctx* ctx, const tsm_batch* b, char* err, size_t errlen
         return set_err(err, errlen, "batch->usable %u exceeds row_stride %u", b->usable, b->row_stride), 1;
     if ((b->hist_ids == nullptr) != (b->hist_offsets == nullptr))
         return set_err(err, errlen, "hist_ids and hist_offsets must both be set or both be NULL"), 1;
+    if (b->row_kinds & ~(TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE))
+        return set_err(err, errlen, "batch->row_kinds 0x%x has unknown bits", b->row_kinds), 1;
+    if (b->reserved != 0) return set_err(err, errlen, "batch->reserved must be 0"), 1;
     if (b->mask && b->mask_stride < (b->usable + 31) / 32)
         return set_err(err, errlen, "mask_stride %u is below ceil(usable/32) = %u", b->mask_stride,
                        (b->usable + 31) / 32), 1;
@@ -61,7 +67,13 @@ int check_batch(const tsm_ctx* ctx, const tsm_batch* b, char* err, size_t errlen
 
 extern "C" {
 
-const char* tsm_version(void) { return "tachyon-sampler 0.1 gfx950"; }
+const char* tsm_version(void) { return "tachyon-sampler 0.2 gfx950"; }
+
+uint32_t tsm_row_kind(const tsm_row_params* p, uint32_t usable, uint32_t hist_len, int has_mask) {
+    if (!p || usable == 0) return TSM_ROWKIND_WHOLE;
+    const tsm::RowMode m = tsm::row_mode(*p, usable, hist_len, has_mask != 0);
+    return tsm::split::takes_row(m, hist_len) ? TSM_ROWKIND_SPLIT : TSM_ROWKIND_WHOLE;
+}
 
 tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err, size_t errlen) {
     if (max_rows == 0 || max_rows > 65535) {
@@ -96,8 +108,14 @@ tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err
     c->max_rows = max_rows;
     c->max_vocab = max_vocab;
     c->status = nullptr;
+    c->split_mem = nullptr;
     hipError_t e = hipMalloc(&c->status, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
+    const size_t sb = tsm::split::scratch_bytes(max_rows, max_vocab);
+    if (e == hipSuccess) e = hipMalloc(&c->split_mem, sb);
+    // the row counters must start at 0; the kernel returns them to 0
+    if (e == hipSuccess) e = hipMemset(c->split_mem, 0, sb);
+    if (e == hipSuccess) c->split = tsm::split::scratch_carve(c->split_mem, max_rows, max_vocab);
     if (e == hipSuccess) e = tsm::sample_set_smem_attr();
     if (e != hipSuccess) {
         set_err(err, errlen, "device setup failed: %s", hipGetErrorString(e));
@@ -112,6 +130,7 @@ void tsm_destroy(tsm_ctx* ctx) {
     DeviceGuard g(ctx->device);
     (void)hipDeviceSynchronize();
     if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->split_mem) (void)hipFree(ctx->split_mem);
     delete ctx;
 }
 
@@ -151,7 +170,25 @@ static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs
         a.out_prob = out->prob;
         a.out_keep = out->keep;
     }
-    tsm::launch_sample(a, b->rows, vec, s);
+    // one kernel per row kind the batch holds (both when it does not say).
+    // The split-row kernel pays off for small batches, where one workgroup
+    // per row would leave most of the chip idle; from kSplitRowsMax rows on,
+    // the whole-row kernel samples every row (it takes every kind).
+    uint32_t kinds = b->row_kinds ? b->row_kinds : (TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE);
+    if (b->rows > tsm::split::kSplitRowsMax) kinds = TSM_ROWKIND_WHOLE;
+    if (kinds & TSM_ROWKIND_SPLIT) {
+        tsm::split::SplitArgs sa;
+        sa.s = a;
+        sa.w = ctx->split;
+        sa.seg_len = tsm::split::pick_seg_len(b->rows, b->usable);
+        sa.nseg = (b->usable + sa.seg_len - 1) / sa.seg_len;
+        sa.general = (kinds & TSM_ROWKIND_WHOLE) ? 1u : 0u;
+        tsm::split::launch(sa, b->rows, vec, s);
+    }
+    if (kinds & TSM_ROWKIND_WHOLE) {
+        a.skip_split = (kinds & TSM_ROWKIND_SPLIT) ? 1u : 0u;
+        tsm::launch_sample(a, b->rows, vec, s);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "kernel launch failed: %s", hipGetErrorString(e)), 1;
     return 0;

@@ -24,6 +24,7 @@ struct SampleArgs {
     float* dist_probs;
     uint32_t row_stride, usable, mask_stride, top_stride, dist_stride;
     uint32_t distribution;  // 1: write the kept distribution instead of drawing
+    uint32_t skip_split;    // 1: rows the split kernel takes are sampled there (this kernel skips them)
 };
 
 // Queues one sampling step (one workgroup per row) on `stream`.

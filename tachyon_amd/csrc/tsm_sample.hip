@@ -35,6 +35,7 @@
 // and slower.
 #include "tsm_sample.h"
 #include "tsm_select.h"
+#include "tsm_split.h"
 
 namespace tsm {
 
@@ -1718,6 +1719,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     f.mrow = f.m.constrained ? a.mask + static_cast<size_t>(row) * a.mask_stride : nullptr;
     f.P = P;
     const RowMode m = f.m;  // register copies: f escapes to the re-read functions
+    if (a.skip_split && split::takes_row(m, hlen)) return;  // sampled by split_kernel
     const float* rowp = f.rowp;
     uint32_t* misc = lds_misc();
     uint2* buf = lds_buf();

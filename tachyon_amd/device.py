@@ -29,6 +29,8 @@ class DeviceBatch:
     mask: "object"
     uniforms: "object"
     top_stride: int
+    row_kinds: int = 0          # OR of tsm_row_kind() over the rows (0: not known)
+    dist_kinds: int = 0         # the same for tsm_distribution() (masks do not apply)
 
     @property
     def rows(self):
@@ -43,7 +45,21 @@ class DeviceBatch:
         return 0 if self.mask is None else int(self.mask.shape[1])
 
 
-def upload(w: Workload, device="cuda:0") -> DeviceBatch:
+def row_kinds(w: Workload, has_mask: bool) -> int:
+    """OR of tsm_row_kind() over the workload's rows, from its host-side
+    parameters and history lengths (what a caller knows before the step)."""
+    L = _lib.lib()
+    params = np.ascontiguousarray(w.params)
+    hl = np.zeros(w.rows, np.int64) if w.hist_offsets is None else np.diff(w.hist_offsets.astype(np.int64))
+    kinds = 0
+    base = params.ctypes.data
+    for r in range(w.rows):
+        kinds |= int(L.tsm_row_kind(ctypes.c_void_p(base + r * params.itemsize), w.usable, int(hl[r]),
+                                    1 if has_mask else 0))
+    return kinds
+
+
+def upload(w: Workload, device="cuda:0", kinds=True) -> DeviceBatch:
     import torch
 
     def t(a, dtype=None):
@@ -57,7 +73,9 @@ def upload(w: Workload, device="cuda:0") -> DeviceBatch:
         hist_ids=t(w.hist_ids.view(np.int32)) if w.hist_ids is not None else None,
         hist_offsets=t(w.hist_offsets.view(np.int32)) if w.hist_offsets is not None else None,
         mask=t(w.mask.view(np.int32)) if w.mask is not None else None,
-        uniforms=t(w.uniforms), top_stride=max(1, w.top_stride))
+        uniforms=t(w.uniforms), top_stride=max(1, w.top_stride),
+        row_kinds=row_kinds(w, w.mask is not None) if kinds else 0,
+        dist_kinds=row_kinds(w, False) if kinds else 0)
 
 
 class Outputs:
@@ -105,7 +123,8 @@ class SamplerContext:
     def _batch(self, b: DeviceBatch, uniforms=True):
         return _lib.TsmBatch(
             _ptr(b.logits), b.rows, b.row_stride, b.usable, b.mask_stride, _ptr(b.params),
-            _ptr(b.hist_ids), _ptr(b.hist_offsets), _ptr(b.mask), _ptr(b.uniforms) if uniforms else None)
+            _ptr(b.hist_ids), _ptr(b.hist_offsets), _ptr(b.mask), _ptr(b.uniforms) if uniforms else None,
+            b.row_kinds if uniforms else b.dist_kinds, 0)
 
     def sample(self, b: DeviceBatch, out: Outputs, stream=None, with_prob=True, with_keep=True,
                with_logprobs=True):
@@ -147,11 +166,12 @@ class SamplerContext:
         return int(st.value)
 
 
-def run_workload(ctx: SamplerContext, w: Workload, device="cuda:0"):
-    """Uploads `w`, samples every row on the GPU, returns numpy outputs."""
+def run_workload(ctx: SamplerContext, w: Workload, device="cuda:0", kinds=True):
+    """Uploads `w`, samples every row on the GPU, returns numpy outputs.
+    kinds=False leaves the batch's row kinds unknown (every kernel queued)."""
     import torch
 
-    b = upload(w, device)
+    b = upload(w, device, kinds=kinds)
     out = Outputs(w.rows, max(1, w.top_stride), device)
     ctx.sample(b, out)
     torch.cuda.synchronize()

@@ -6,7 +6,9 @@
 //
 // Input (little endian): u32 magic 'TSMW', mode (0 sample, 1 distribution),
 // rows, row_stride, usable, mask_stride (0: no mask), hist_total
-// (0xFFFFFFFF: no history), top_stride, dist_stride, reserved; then
+// (0xFFFFFFFF: no history), top_stride, dist_stride, kinds (0: the batch's
+// row_kinds left unknown, 1: computed with tsm_row_kind as a caller would);
+// then
 // logits f32[rows*row_stride], params (40 B each)[rows],
 // hist_offsets u32[rows+1] + hist_ids u32[hist_total] (if history),
 // mask u32[rows*mask_stride] (if mask), uniforms f32[rows].
@@ -63,7 +65,7 @@ int main(int argc, char** argv) {
     if (R.u32() != 0x574D5354u) return 3;
     const uint32_t mode = R.u32(), rows = R.u32(), row_stride = R.u32(), usable = R.u32();
     const uint32_t mask_stride = R.u32(), hist_total = R.u32(), top_stride = R.u32(), dist_stride = R.u32();
-    (void)R.u32();
+    const uint32_t kinds_mode = R.u32();
     tsm_batch b{};
     b.logits = R.dev<float>(static_cast<size_t>(rows) * row_stride);
     b.rows = rows;
@@ -77,6 +79,12 @@ int main(int argc, char** argv) {
     }
     if (mask_stride) b.mask = R.dev<uint32_t>(static_cast<size_t>(rows) * mask_stride);
     b.uniforms = R.dev<float>(rows);
+    if (kinds_mode == 1) {  // as a caller would: from the host-side parameters and history lengths
+        for (uint32_t r = 0; r < rows; r++) {
+            const uint32_t hl = b.hist_offsets ? b.hist_offsets[r + 1] - b.hist_offsets[r] : 0u;
+            b.row_kinds |= tsm_row_kind(&b.params[r], usable, hl, mode == 0 && b.mask != nullptr);
+        }
+    }
     std::fclose(in);
 
     char err[512] = {0};

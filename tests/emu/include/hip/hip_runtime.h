@@ -97,6 +97,9 @@ inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; 
 inline long long __double_as_longlong(double d) { long long u; std::memcpy(&u, &d, 8); return u; }
 inline double __longlong_as_double(long long u) { double d; std::memcpy(&d, &u, 8); return d; }
 inline int __popc(uint32_t v) { return __builtin_popcount(v); }
+inline uint32_t __builtin_amdgcn_ubfe(uint32_t v, uint32_t off, uint32_t w) {
+    return w >= 32 ? v >> off : (v >> off) & ((1u << w) - 1u);
+}
 inline int __popcll(uint64_t v) { return __builtin_popcountll(v); }
 inline int __clz(uint32_t v) { return v ? __builtin_clz(v) : 32; }
 inline int __ffs(uint32_t v) { return __builtin_ffs(v); }
@@ -167,6 +170,8 @@ inline uint32_t __builtin_amdgcn_mbcnt_hi(uint32_t mask, uint32_t acc) {
     return acc + static_cast<uint32_t>(__builtin_popcount(mask & below));
 }
 #define __HIP_MEMORY_SCOPE_WORKGROUP 3
+#define __HIP_MEMORY_SCOPE_AGENT 4
+#define __builtin_amdgcn_s_waitcnt(n) ((void)(n))
 inline std::memory_order emu_order(int order) {
     switch (order) {
         case __ATOMIC_RELAXED: return std::memory_order_relaxed;
@@ -187,12 +192,24 @@ inline T __hip_atomic_load(T* p, int, int) {
     return std::atomic_ref<T>(*p).load(std::memory_order_acquire);
 }
 template <class T>
+inline void __hip_atomic_store(T* p, T v, int, int) {
+    std::atomic_ref<T>(*p).store(v, std::memory_order_release);
+}
+template <class T>
+inline T __hip_atomic_fetch_add(T* p, T v, int, int) {
+    return std::atomic_ref<T>(*p).fetch_add(v, std::memory_order_acq_rel);
+}
+template <class T>
 inline T __hip_atomic_fetch_max(T* p, T v, int, int) {
     std::atomic_ref<T> a(*p);
     T old = a.load(std::memory_order_relaxed);
     while (!a.compare_exchange_weak(old, old > v ? old : v, std::memory_order_acq_rel, std::memory_order_relaxed)) {}
     return old;
 }
+
+// Device-scope fence: blocks run one after another here, so it only has to
+// order this thread's own memory operations.
+inline void __threadfence() { std::atomic_thread_fence(std::memory_order_seq_cst); }
 
 template <class T>
 inline T __shfl_xor(T v, int mask, int width = 64) {

@@ -29,12 +29,12 @@ def build(target="emu_driver"):
     return os.path.join(EMU_DIR, target)
 
 
-def _write_input(path, w, mode, dist_stride=0):
+def _write_input(path, w, mode, dist_stride=0, kinds=1):
     hist_total = 0xFFFFFFFF if w.hist_ids is None else int(w.hist_ids.size)
     mask_stride = 0 if w.mask is None else int(w.mask.shape[1])
     with open(path, "wb") as fh:
         fh.write(struct.pack("<10I", 0x574D5354, mode, w.rows, w.row_stride, w.usable, mask_stride, hist_total,
-                             int(w.top_stride), int(dist_stride), 0))
+                             int(w.top_stride), int(dist_stride), int(kinds)))
         fh.write(np.ascontiguousarray(w.logits, np.float32).tobytes())
         fh.write(np.ascontiguousarray(w.params).tobytes())
         if w.hist_ids is not None:
@@ -49,13 +49,13 @@ class EmuError(RuntimeError):
     pass
 
 
-def _run(w, mode, dist_stride=0, driver=None, timeout=900):
+def _run(w, mode, dist_stride=0, driver=None, timeout=900, kinds=1):
     driver = driver or DRIVER
     if not os.path.exists(driver):
         build(os.path.basename(driver))
     with tempfile.TemporaryDirectory() as d:
         fin, fout = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
-        _write_input(fin, w, mode, dist_stride)
+        _write_input(fin, w, mode, dist_stride, kinds)
         env = dict(os.environ)
         env.setdefault("ASAN_OPTIONS", "detect_leaks=0:abort_on_error=1")
         r = subprocess.run([driver, fin, fout], capture_output=True, text=True, timeout=timeout, env=env)

@@ -105,6 +105,62 @@ def test_parity_baseline_configs(ctx, name):
     check_mask_property(w, got)
 
 
+def _rows_of(w, sel, name):
+    """The rows `sel` of workload w (with their histories) as a workload."""
+    hist_ids = hist_off = None
+    if w.hist_offsets is not None:
+        lens = np.diff(w.hist_offsets.astype(np.int64))[sel]
+        hist_off = np.zeros(len(sel) + 1, np.uint32)
+        hist_off[1:] = np.cumsum(lens)
+        hist_ids = np.concatenate([w.hist_ids[w.hist_offsets[r]:w.hist_offsets[r + 1]] for r in sel]).astype(np.uint32)
+    return wl.Workload(name, np.ascontiguousarray(w.logits[sel]), w.usable, w.params[sel].copy(), hist_ids, hist_off,
+                       None if w.mask is None else np.ascontiguousarray(w.mask[sel]), w.uniforms[sel].copy(),
+                       top_stride=w.top_stride)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
+@pytest.mark.parametrize("kinds", [True, False], ids=["kinds", "nokinds"])
+def test_parity_split_path(ctx, name, kinds):
+    """Batches of at most 16 rows take the split-row kernel for their top-k
+    rows: the BASELINE shapes at full vocabulary, 16 rows (c2: two of each
+    row kind), with the batch's row kinds given and left unknown."""
+    from oracle import pyoracle
+    from tachyon_amd.device import run_workload
+
+    full = wl.CONFIGS[name]()
+    sel = np.arange(0, full.rows, max(1, full.rows // 16))[:16] if name != "c2" else np.array(
+        [0, 1, 8, 9, 16, 17, 24, 25])
+    w = _rows_of(full, sel, f"{name}s")
+    say(f"[gpu] split path {name}: rows={w.rows} kinds={kinds}")
+    got = run_workload(ctx, w, kinds=kinds)
+    assert ctx.status() == 0
+    ref = pyoracle.sample_batch(w, nthreads=16)
+    exact_rows, exempt, _ = check(w, got, ref, f"split {name}")
+    check_mask_property(w, got)
+    say(f"[gpu] split path {name}: ok, exact rows {exact_rows}/{w.rows}, boundary-exempt {exempt}")
+
+
+def test_split_path_row_kind_mismatch(ctx):
+    """A small batch that names only the split kind but holds a row without
+    top-k: that row is not sampled and the status says so; the others are."""
+    from oracle import pyoracle
+    from tachyon_amd import _lib
+    from tachyon_amd.device import Outputs, upload
+
+    w = wl.random_case(seed=41, vocab=3000, rows=6, mode="topk")
+    w.params["top_k"][3] = 0  # no top-k: the whole-row kind
+    b = upload(w)
+    b.row_kinds = _lib.ROWKIND_SPLIT
+    out = Outputs(w.rows, w.top_stride)
+    ctx.sample(b, out)
+    got = out.numpy()
+    assert ctx.status() & 16  # TSM_STATUS_ROW_KIND
+    ref = pyoracle.sample_batch(w)
+    for r in range(w.rows):
+        if r != 3:
+            assert got["token"][r] == ref.token[r], r
+
+
 def test_parity_c5_nucleus(ctx):
     w = wl.c5()
     run_case(ctx, w, "c5")
