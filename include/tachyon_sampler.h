@@ -179,6 +179,22 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
                                           left out: token 0 written           */
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);
 
+/*
+ * tsm_sample() without a context and without allocating anything: for
+ * callers that cannot call hipMalloc (code under HIP graph capture, serving
+ * loops and harnesses that forbid it).  It has no counterpart in the
+ * reference.  Its scratch is a fixed array in the library's device memory,
+ * one per GPU (about 25 MB, held until the process ends), which takes batches
+ * of up to 16 rows of up to 2^18 ids on the split-row kernel; other batches
+ * (up to 65535 rows of up to TSM_MAX_VOCAB ids) take the whole-row kernel,
+ * which needs no scratch.  Larger batches are rejected.  Works on the current
+ * HIP device.  `status` (a device word, may be NULL) is cleared and then
+ * receives this call's TSM_STATUS_* bits.  Calls on one GPU share its scratch:
+ * calls that overlap on one GPU (other streams, other threads) race.
+ */
+int tsm_sample_static(void* stream, const tsm_batch* batch, const tsm_outputs* out,
+                      uint32_t* status, char* err, size_t errlen);
+
 /* The kind (TSM_ROWKIND_*) of a row: `p` is the row's parameters (host
  * memory), `usable` the batch's, `hist_len` the row's history length,
  * `has_mask` whether the batch passes a mask. */

@@ -47,7 +47,7 @@ class TsmOutputs(ctypes.Structure):
 
 
 SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version",
-           "tsm_row_kind"]
+           "tsm_row_kind", "tsm_sample_static"]
 ROWKIND_SPLIT = 1
 ROWKIND_WHOLE = 2
 
@@ -80,6 +80,9 @@ def lib():
         L.tsm_status.argtypes = [vp, ctypes.POINTER(u32), ctypes.c_char_p, ctypes.c_size_t]
         L.tsm_version.restype = ctypes.c_char_p
         L.tsm_version.argtypes = []
+        L.tsm_sample_static.restype = ctypes.c_int
+        L.tsm_sample_static.argtypes = [vp, ctypes.POINTER(TsmBatch), ctypes.POINTER(TsmOutputs), vp,
+                                        ctypes.c_char_p, ctypes.c_size_t]
         L.tsm_row_kind.restype = u32
         L.tsm_row_kind.argtypes = [vp, u32, u32, ctypes.c_int]
         _lib = L

@@ -3,6 +3,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "tsm_sample.h"
 #include "tsm_split.h"
@@ -39,17 +40,16 @@ struct DeviceGuard {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_batch(const tsm_ctx* ctx, const tsm_batch* b, char* err, size_t errlen) {
-    if (!ctx) return set_err(err, errlen, "context is NULL"), 1;
+int check_batch(uint32_t max_rows, uint32_t max_vocab, const tsm_batch* b, char* err, size_t errlen) {
     if (!b) return set_err(err, errlen, "batch is NULL"), 1;
     if (!b->logits) return set_err(err, errlen, "batch->logits is NULL"), 1;
     if (!b->params) return set_err(err, errlen, "batch->params is NULL"), 1;
     if (b->rows == 0) return set_err(err, errlen, "batch->rows is 0"), 1;
-    if (b->rows > ctx->max_rows)
-        return set_err(err, errlen, "batch->rows %u exceeds the context's max_rows %u", b->rows, ctx->max_rows), 1;
+    if (b->rows > max_rows)
+        return set_err(err, errlen, "batch->rows %u exceeds the maximum of %u", b->rows, max_rows), 1;
     if (b->usable == 0) return set_err(err, errlen, "batch->usable is 0"), 1;
-    if (b->usable > ctx->max_vocab)
-        return set_err(err, errlen, "batch->usable %u exceeds the context's max_vocab %u", b->usable, ctx->max_vocab), 1;
+    if (b->usable > max_vocab)
+        return set_err(err, errlen, "batch->usable %u exceeds the maximum of %u", b->usable, max_vocab), 1;
     if (b->usable > b->row_stride)
         return set_err(err, errlen, "batch->usable %u exceeds row_stride %u", b->usable, b->row_stride), 1;
     if ((b->hist_ids == nullptr) != (b->hist_offsets == nullptr))
@@ -60,6 +60,61 @@ int check_batch(const tsm_ctx* ctx, const tsm_batch* b, char* err, size_t errlen
     if (b->mask && b->mask_stride < (b->usable + 31) / 32)
         return set_err(err, errlen, "mask_stride %u is below ceil(usable/32) = %u", b->mask_stride,
                        (b->usable + 31) / 32), 1;
+    return 0;
+}
+
+// ---- the allocation-free entry point's scratch ------------------------------------
+// tsm_sample_static allocates nothing: the split kernel's records for batches
+// of up to kStaticRows rows of up to kStaticVocab ids, and a status word, live
+// in this file-scope array (each GPU the library runs on holds its own copy
+// until the process ends).  Host code never passes `scratch` itself to a
+// kernel: its device address comes from hipGetSymbolAddress, once per device.
+constexpr uint32_t kStaticRows = tsm::split::kSplitRowsMax;
+constexpr uint32_t kStaticVocab = 1u << 18;
+constexpr uint64_t kStaticSplitBytes = tsm::split::scratch_bytes(kStaticRows, kStaticVocab);
+constexpr uint64_t kStaticBytes = kStaticSplitBytes + 256;  // + the status word
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+constexpr uint32_t kStaticMaxRows = 65535;  // the whole-row kernel needs no scratch but the status word
+constexpr int kMaxDevices = 64;
+struct StaticDev {
+    void* ptr = nullptr;  // device address of `scratch` on this device
+    bool ready = false;
+};
+StaticDev g_static[kMaxDevices];
+std::mutex g_static_mu;
+
+// Clears n words (a fill kernel rather than a memset, so that a caller may
+// capture the call in a graph).
+__global__ void clear_words(uint32_t* p, uint32_t n) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// The current device's scratch address and kernel attributes, set up on its
+// first call.
+int static_setup(int* dev_out, void** ptr_out, char* err, size_t errlen) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return set_err(err, errlen, "no current HIP device"), 1;
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    StaticDev& d = g_static[dev];
+    if (!d.ready) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+            return set_err(err, errlen, "hipGetDeviceProperties failed"), 1;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            return set_err(err, errlen, "device %d is %s; this library is built for gfx950", dev, prop.gcnArchName), 1;
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_err(err, errlen, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e)), 1;
+        const hipError_t e2 = tsm::sample_set_smem_attr();
+        if (e2 != hipSuccess) return set_err(err, errlen, "kernel attribute setup failed: %s", hipGetErrorString(e2)), 1;
+        d.ptr = p;
+        d.ready = true;
+    }
+    *dev_out = dev;
+    *ptr_out = d.ptr;
     return 0;
 }
 
@@ -111,11 +166,13 @@ tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err
     c->split_mem = nullptr;
     hipError_t e = hipMalloc(&c->status, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
-    const size_t sb = tsm::split::scratch_bytes(max_rows, max_vocab);
+    // the split kernel runs for batches of at most kSplitRowsMax rows
+    const uint32_t split_rows = max_rows < tsm::split::kSplitRowsMax ? max_rows : tsm::split::kSplitRowsMax;
+    const size_t sb = tsm::split::scratch_bytes(split_rows, max_vocab);
     if (e == hipSuccess) e = hipMalloc(&c->split_mem, sb);
     // the row counters must start at 0; the kernel returns them to 0
     if (e == hipSuccess) e = hipMemset(c->split_mem, 0, sb);
-    if (e == hipSuccess) c->split = tsm::split::scratch_carve(c->split_mem, max_rows, max_vocab);
+    if (e == hipSuccess) c->split = tsm::split::scratch_carve(c->split_mem, split_rows, max_vocab);
     if (e == hipSuccess) e = tsm::sample_set_smem_attr();
     if (e != hipSuccess) {
         set_err(err, errlen, "device setup failed: %s", hipGetErrorString(e));
@@ -134,13 +191,11 @@ void tsm_destroy(tsm_ctx* ctx) {
     delete ctx;
 }
 
-static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs* out, uint32_t* dist_ids,
-               float* dist_probs, uint32_t dist_stride, uint32_t* keep, bool distribution, char* err,
-               size_t errlen) {
-    if (check_batch(ctx, b, err, errlen)) return 1;
-    DeviceGuard g(ctx->device);
-    if (!g.ok) return set_err(err, errlen, "hipSetDevice(%d) failed", ctx->device), 1;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+// Queues one step: the split kernel for the batch's split-kind rows (small
+// batches, when `split` is given), the whole-row kernel for the others.
+static int queue(hipStream_t s, const tsm_batch* b, const tsm_outputs* out, uint32_t* dist_ids, float* dist_probs,
+                 uint32_t dist_stride, uint32_t* keep, bool distribution, uint32_t* status,
+                 const tsm::split::SplitScratch* split, char* err, size_t errlen) {
     const bool vec = (b->row_stride % 4 == 0) && aligned16(b->logits);
 
     tsm::SampleArgs a;
@@ -151,7 +206,7 @@ static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs
     a.hist_off = b->hist_offsets;
     a.mask = distribution ? nullptr : b->mask;
     a.uniforms = b->uniforms;
-    a.status = ctx->status;
+    a.status = status;
     a.row_stride = b->row_stride;
     a.usable = b->usable;
     a.mask_stride = b->mask_stride;
@@ -175,11 +230,11 @@ static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs
     // per row would leave most of the chip idle; from kSplitRowsMax rows on,
     // the whole-row kernel samples every row (it takes every kind).
     uint32_t kinds = b->row_kinds ? b->row_kinds : (TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE);
-    if (b->rows > tsm::split::kSplitRowsMax) kinds = TSM_ROWKIND_WHOLE;
+    if (b->rows > tsm::split::kSplitRowsMax || !split) kinds = TSM_ROWKIND_WHOLE;
     if (kinds & TSM_ROWKIND_SPLIT) {
         tsm::split::SplitArgs sa;
         sa.s = a;
-        sa.w = ctx->split;
+        sa.w = *split;
         sa.seg_len = tsm::split::pick_seg_len(b->rows, b->usable);
         sa.nseg = (b->usable + sa.seg_len - 1) / sa.seg_len;
         sa.general = (kinds & TSM_ROWKIND_WHOLE) ? 1u : 0u;
@@ -192,6 +247,17 @@ static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "kernel launch failed: %s", hipGetErrorString(e)), 1;
     return 0;
+}
+
+static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs* out, uint32_t* dist_ids,
+               float* dist_probs, uint32_t dist_stride, uint32_t* keep, bool distribution, char* err,
+               size_t errlen) {
+    if (!ctx) return set_err(err, errlen, "context is NULL"), 1;
+    if (check_batch(ctx->max_rows, ctx->max_vocab, b, err, errlen)) return 1;
+    DeviceGuard g(ctx->device);
+    if (!g.ok) return set_err(err, errlen, "hipSetDevice(%d) failed", ctx->device), 1;
+    return queue(static_cast<hipStream_t>(stream), b, out, dist_ids, dist_probs, dist_stride, keep, distribution,
+                 ctx->status, &ctx->split, err, errlen);
 }
 
 int tsm_sample(tsm_ctx* ctx, void* stream, const tsm_batch* batch, const tsm_outputs* out, char* err,
@@ -222,6 +288,32 @@ int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen) {
     if (e == hipSuccess) e = hipMemset(ctx->status, 0, sizeof(uint32_t));
     if (e != hipSuccess) return set_err(err, errlen, "status read failed: %s", hipGetErrorString(e)), 1;
     return 0;
+}
+
+int tsm_sample_static(void* stream, const tsm_batch* batch, const tsm_outputs* out, uint32_t* status, char* err,
+                      size_t errlen) {
+    if (!out || !out->token) return set_err(err, errlen, "outputs->token is NULL"), 1;
+    if (batch && !batch->uniforms) return set_err(err, errlen, "batch->uniforms is NULL"), 1;
+    if ((out->top_ids || out->top_logprobs) && out->top_stride == 0)
+        return set_err(err, errlen, "top_stride is 0 while top_ids/top_logprobs are given"), 1;
+    if (out->top_logprobs && !out->top_ids) return set_err(err, errlen, "top_logprobs needs top_ids"), 1;
+    if (out->top_stride > TSM_MAX_LOGPROBS && (out->top_ids || out->top_logprobs))
+        return set_err(err, errlen, "top_stride %u exceeds TSM_MAX_LOGPROBS", out->top_stride), 1;
+    if (check_batch(kStaticMaxRows, TSM_MAX_VOCAB, batch, err, errlen)) return 1;
+    int dev = -1;
+    void* base = nullptr;
+    if (static_setup(&dev, &base, err, errlen)) return 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    unsigned char* p = static_cast<unsigned char*>(base);
+    uint32_t* st = status ? status : reinterpret_cast<uint32_t*>(p + kStaticSplitBytes);
+    // the split kernel takes batches the scratch holds; others go whole
+    const bool fits = batch->rows <= kStaticRows && batch->usable <= kStaticVocab;
+    tsm::split::SplitScratch w = tsm::split::scratch_carve(p, kStaticRows, kStaticVocab);
+    // what must start at 0: the row counters (a previous call returned them
+    // to 0 unless it was cut short) and the status word
+    hipLaunchKernelGGL(clear_words, dim3(1), dim3(256), 0, s, reinterpret_cast<uint32_t*>(w.row_ctr), 2u * kStaticRows);
+    hipLaunchKernelGGL(clear_words, dim3(1), dim3(64), 0, s, st, 1u);
+    return queue(s, batch, out, nullptr, nullptr, 0, nullptr, false, st, fits ? &w : nullptr, err, errlen);
 }
 
 }  // extern "C"

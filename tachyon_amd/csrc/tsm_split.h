@@ -56,8 +56,26 @@ struct SplitArgs {
     uint32_t general;      // 1: rows this kernel does not take are sampled by sample_kernel
 };
 
-// Device scratch bytes for `rows` rows of `vocab` ids.
-size_t scratch_bytes(uint32_t rows, uint32_t vocab);
+constexpr uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+constexpr uint64_t align256(uint64_t b) { return (b + 255) & ~static_cast<uint64_t>(255); }
+// The most segments a call of up to `rows` rows of up to `vocab` ids asks for.
+// With L = pick_seg_len(r, u) >= kSegMin, a call has r * ceil(u / L) <= rows *
+// ceil(vocab / kSegMin) segments; and L = kSegMax gives rows * ceil(vocab /
+// kSegMax), while L between kSegMin and kSegMax (rounded up from r * u / 2048)
+// or L = kSegMin (only when r * u <= 2048 * kSegMin) give at most 2048 + r.
+constexpr uint64_t max_segments(uint32_t rows, uint32_t vocab) {
+    const uint64_t big = static_cast<uint64_t>(rows) * ceil_div(vocab, kSegMax);
+    const uint64_t mid = 2048u + 2ull * rows;
+    const uint64_t lim = static_cast<uint64_t>(rows) * ceil_div(vocab, kSegMin);
+    const uint64_t b = big > mid ? big : mid;
+    return b < lim ? b : lim;
+}
+// Device scratch bytes for `rows` rows of `vocab` ids (the layout of scratch_carve).
+constexpr uint64_t scratch_bytes(uint32_t rows, uint32_t vocab) {
+    return align256(max_segments(rows, vocab) * sizeof(SegSum)) +
+           align256(max_segments(rows, vocab) * kCandCap * sizeof(uint2)) +
+           align256(static_cast<uint64_t>(rows) * kSplitHist * sizeof(uint2)) + align256(rows * 8ull);
+}
 // Carves `base` (scratch_bytes(rows, vocab) bytes) into the scratch record.
 SplitScratch scratch_carve(void* base, uint32_t rows, uint32_t vocab);
 // Segment length the host picks for a batch (a multiple of kSegQuant).
@@ -70,8 +88,6 @@ __host__ __device__ inline bool takes_row(const RowMode& m, uint32_t hist_len) {
     const uint32_t h = m.penal ? hist_len : 0u;
     return m.topk && h <= kSplitHist && m.window + h <= kSplitNeed;
 }
-// Segments a context for `rows` rows of `vocab` ids may be asked for.
-uint64_t max_segments(uint32_t rows, uint32_t vocab);
 // Queues one step of the split kernel on `stream`.
 void launch(const SplitArgs& a, uint32_t rows, bool vec_loads, hipStream_t stream);
 

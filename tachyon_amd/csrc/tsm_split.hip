@@ -1616,7 +1616,6 @@ template __global__ void split_kernel<true>(SplitArgs);
 template __global__ void split_kernel<false>(SplitArgs);
 
 // ---- host side ---------------------------------------------------------------------
-static uint32_t segs_for(uint32_t vocab, uint32_t seg_len) { return (vocab + seg_len - 1) / seg_len; }
 
 uint32_t pick_seg_len(uint32_t rows, uint32_t usable) {
     // about 2048 workgroups per step (8 per CU), each segment between kSegMin
@@ -1630,24 +1629,6 @@ uint32_t pick_seg_len(uint32_t rows, uint32_t usable) {
     len = (len + kSegQuant - 1) / kSegQuant * kSegQuant;
     if (len > kSegMax) len = kSegMax;
     return static_cast<uint32_t>(len);
-}
-
-static size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
-
-// The most segments a call may ask for.  With L = pick_seg_len(rows, usable):
-// L = kSegMax gives rows * ceil(usable / kSegMax); between kSegMin and kSegMax
-// (rounded up from rows * usable / 2048), at most 2048 + rows; L = kSegMin
-// only when rows * usable <= 2048 * kSegMin, again at most 2048 + rows.
-uint64_t max_segments(uint32_t rows, uint32_t vocab) {
-    const uint64_t big = static_cast<uint64_t>(rows) * segs_for(vocab, kSegMax);
-    const uint64_t mid = 2048u + 2ull * rows;
-    return big > mid ? big : mid;
-}
-
-size_t scratch_bytes(uint32_t rows, uint32_t vocab) {
-    const uint64_t segs = max_segments(rows, vocab);
-    return align256(segs * sizeof(SegSum)) + align256(segs * kCandCap * sizeof(uint2)) +
-           align256(static_cast<size_t>(rows) * kSplitHist * sizeof(uint2)) + align256(rows * 8u);
 }
 
 SplitScratch scratch_carve(void* base, uint32_t rows, uint32_t vocab) {

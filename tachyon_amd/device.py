@@ -166,6 +166,27 @@ class SamplerContext:
         return int(st.value)
 
 
+def _outputs(out: Outputs):
+    return _lib.TsmOutputs(_ptr(out.token), _ptr(out.logprob), _ptr(out.top_ids), _ptr(out.top_lp), out.top_stride,
+                           0, _ptr(out.prob), _ptr(out.keep))
+
+
+def sample_static(b: DeviceBatch, out: Outputs, status=None, stream=None):
+    """tsm_sample_static(): one step with no context and no allocation; status
+    (an int32 cuda tensor of one element, or None) gets the call's status bits."""
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    bb = _lib.TsmBatch(_ptr(b.logits), b.rows, b.row_stride, b.usable, b.mask_stride, _ptr(b.params),
+                       _ptr(b.hist_ids), _ptr(b.hist_offsets), _ptr(b.mask), _ptr(b.uniforms), b.row_kinds, 0)
+    ob = _outputs(out)
+    err = _lib._err()
+    rc = _lib.lib().tsm_sample_static(ctypes.c_void_p(s), ctypes.byref(bb), ctypes.byref(ob), _ptr(status), err,
+                                      len(err))
+    if rc != 0:
+        raise _lib.TsmError(err.value.decode())
+
+
 def run_workload(ctx: SamplerContext, w: Workload, device="cuda:0", kinds=True):
     """Uploads `w`, samples every row on the GPU, returns numpy outputs.
     kinds=False leaves the batch's row kinds unknown (every kernel queued)."""
