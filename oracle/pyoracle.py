@@ -39,28 +39,17 @@ class OrRowDiag(ctypes.Structure):
         ("ranked", ctypes.c_uint32),
         ("survivors", ctypes.c_uint32),
         ("keep", ctypes.c_uint32),
-        ("keep_exact", ctypes.c_uint32),
         ("pick", ctypes.c_uint32),
-        ("pick_exact", ctypes.c_uint32),
         ("consumed_u", ctypes.c_uint32),
-        ("u_gap", ctypes.c_double),
-        ("p_gap", ctypes.c_double),
-        ("mass64", ctypes.c_double),
         ("mass", ctypes.c_float),
         ("best", ctypes.c_float),
-        ("token_exact", ctypes.c_uint32),
-        ("ugap_exact", ctypes.c_double),
-        ("pgap_exact", ctypes.c_double),
     ]
 
 
 DIAG_DTYPE = np.dtype(
     [
         ("path", "<u4"), ("ranked", "<u4"), ("survivors", "<u4"), ("keep", "<u4"),
-        ("keep_exact", "<u4"), ("pick", "<u4"), ("pick_exact", "<u4"),
-        ("consumed_u", "<u4"), ("u_gap", "<f8"), ("p_gap", "<f8"),
-        ("mass64", "<f8"), ("mass", "<f4"), ("best", "<f4"),
-        ("token_exact", "<u4"), ("ugap_exact", "<f8"), ("pgap_exact", "<f8"),
+        ("pick", "<u4"), ("consumed_u", "<u4"), ("mass", "<f4"), ("best", "<f4"),
     ],
     align=True,
 )
@@ -128,6 +117,10 @@ def lib():
         L.or_distribution_batch.restype = ctypes.c_int
         L.or_distribution_batch.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                             vp, vp, vp, vp, vp, ctypes.c_uint32, vp, ctypes.c_int]
+        L.or_reconcile.restype = ctypes.c_int
+        L.or_reconcile.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_size_t, vp, ctypes.c_float,
+                                   ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                   ctypes.POINTER(ctypes.c_double)]
         _lib = L
     return _lib
 
@@ -299,3 +292,23 @@ def distribution_batch(w, dist_stride, nthreads=1):
                                 _vp(w.hist_ids), _vp(w.hist_offsets), _vp(ids), _vp(ps),
                                 dist_stride, _vp(keep), nthreads)
     return ids, ps, keep
+
+
+def reconcile(w, r, token, keep):
+    """How far row r's uniform and top_p must move for the reference to pick
+    `token` with kept count `keep`: (du, dp), or None when no move does."""
+    x = np.ascontiguousarray(w.logits[r, : w.usable], np.float32)
+    prm = np.ascontiguousarray(w.params[r : r + 1])
+    rec = None
+    nrec = 0
+    if w.hist_ids is not None:
+        a, b = int(w.hist_offsets[r]), int(w.hist_offsets[r + 1])
+        rec = np.ascontiguousarray(w.hist_ids[a:b], np.uint32)
+        nrec = b - a
+    m = None
+    if w.mask is not None and (int(w.params["flags"][r]) & 1):
+        m = np.ascontiguousarray(w.mask[r], np.uint32)
+    du, dp = ctypes.c_double(), ctypes.c_double()
+    rc = lib().or_reconcile(_vp(x), w.usable, _vp(prm), _vp(rec) if nrec else None, nrec, _vp(m),
+                            float(w.uniforms[r]), int(token), int(keep), ctypes.byref(du), ctypes.byref(dp))
+    return None if rc else (du.value, dp.value)

@@ -302,79 +302,6 @@ size_t candidates(const or_config& cfg, Scratch& s, const float* logits, size_t 
     return len;
 }
 
-// Exact-arithmetic (f64) view of top-p and the draw, for boundary reporting.
-void exact_view(const or_config& cfg, const Scratch& s, size_t len, size_t keep,
-                size_t pick, float u, bool drew, or_row_diag* d) {
-    std::vector<double> c(len);
-    double acc = 0.0;
-    for (size_t j = 0; j < len; j++) {
-        acc += static_cast<double>(s.probs[j]);
-        c[j] = acc;
-    }
-    const bool greedy = cfg.temperature <= 0.0f;
-    size_t keep_exact = len;
-    d->p_gap = 1.0;
-    if (!greedy && cfg.top_p < 1.0f && len > 0) {
-        const double total = c[len - 1];
-        const double p = cfg.top_p;
-        for (size_t j = 0; j < len; j++)
-            if (c[j] / total >= p) {
-                keep_exact = j + 1;
-                break;
-            }
-        size_t lo = std::min(keep, keep_exact);
-        size_t hi = std::max(keep, keep_exact);
-        lo = lo >= 2 ? lo - 2 : 0;
-        for (size_t j = lo; j < std::min(hi + 1, len); j++)
-            d->p_gap = std::min(d->p_gap, std::fabs(c[j] / total - p));
-        if (keep != keep_exact) d->p_gap = 0.0;
-    }
-    d->keep_exact = static_cast<uint32_t>(keep_exact);
-    // exact arithmetic throughout: the draw over the mass of keep_exact
-    d->token_exact = len > 0 ? s.ri[0] : 0u;
-    d->ugap_exact = 1.0;
-    d->pgap_exact = 1.0;
-    if (!greedy && cfg.top_p < 1.0f && len > 0) {
-        const double total = c[len - 1];
-        const double p = cfg.top_p;
-        double g = std::fabs(c[keep_exact - 1] / total - p);
-        if (keep_exact >= 2) g = std::min(g, std::fabs(c[keep_exact - 2] / total - p));
-        d->pgap_exact = g;
-    }
-    if (drew && keep_exact > 0) {
-        const double m = c[keep_exact - 1];
-        const double target = static_cast<double>(u) * m;
-        size_t pe = keep_exact - 1;
-        for (size_t j = 0; j < keep_exact; j++)
-            if (c[j] >= target) {
-                pe = j;
-                break;
-            }
-        d->token_exact = s.ri[pe];
-        double g = std::fabs(c[pe] - target);
-        if (pe > 0) g = std::min(g, std::fabs(target - c[pe - 1]));
-        d->ugap_exact = g / m;
-    }
-    d->u_gap = 1.0;
-    d->pick_exact = static_cast<uint32_t>(pick);
-    if (drew && keep > 0) {
-        const double mass = c[keep - 1];
-        d->mass64 = mass;
-        const double target = static_cast<double>(u) * mass;
-        size_t pe = keep - 1;
-        for (size_t j = 0; j < keep; j++)
-            if (c[j] >= target) {
-                pe = j;
-                break;
-            }
-        d->pick_exact = static_cast<uint32_t>(pe);
-        double up = c[pick] / mass - u;
-        double gap = std::fabs(up);
-        if (pick > 0) gap = std::min(gap, std::fabs(u - c[pick - 1] / mass));
-        d->u_gap = (pe == pick) ? gap : 0.0;
-    }
-}
-
 // Sampler::pick (sampler.rs:132-151) with the uniform supplied (B.3).
 // Returns the token; *keep_out = keep; prob = p_pick / mass.
 uint32_t pick_impl(const or_config& cfg, Scratch& s, const float* logits, size_t n,
@@ -386,15 +313,8 @@ uint32_t pick_impl(const or_config& cfg, Scratch& s, const float* logits, size_t
         if (prob_out) *prob_out = 1.0f;
         if (d) {
             d->keep = 0;
-            d->keep_exact = 0;
             d->pick = 0;
-            d->pick_exact = 0;
             d->consumed_u = 0;
-            d->u_gap = 1.0;
-            d->p_gap = 1.0;
-            d->ugap_exact = 1.0;
-            d->pgap_exact = 1.0;
-            d->token_exact = or_argmax(logits, n);
         }
         return or_argmax(logits, n);
     }
@@ -415,7 +335,6 @@ uint32_t pick_impl(const or_config& cfg, Scratch& s, const float* logits, size_t
         d->pick = static_cast<uint32_t>(pick);
         d->consumed_u = 1;
         d->mass = mass;
-        exact_view(cfg, s, s.probs.size(), keep, pick, u, true, d);
     }
     return s.ri[pick];
 }
@@ -606,9 +525,7 @@ int or_sample_batch(const float* logits, uint32_t rows, uint32_t row_stride, uin
             kp = 1;
             pr = 1.0f;
             dl.path = OR_PATH_ARGMAX_FAST;
-            dl.ranked = dl.survivors = dl.keep = dl.keep_exact = 1;
-            dl.u_gap = dl.p_gap = dl.ugap_exact = dl.pgap_exact = 1.0;
-            dl.token_exact = tok;
+            dl.ranked = dl.survivors = dl.keep = 1;
         } else {
             tok = pick_impl(cfg, s, x, n, recent, nrecent, mrow, uniforms[r], &kp, &pr, &dl);
         }
@@ -624,6 +541,87 @@ int or_sample_batch(const float* logits, uint32_t rows, uint32_t row_stride, uin
         }
         if (diag) diag[r] = dl;
     });
+    return 0;
+}
+
+// Parity diagnostics (not a reference function): how far u and top_p must
+// move for the reference's own arithmetic to return `token` with kept count
+// `keep`.  The kept count is a step function of top_p: keep = k exactly when
+// acc_{k-1} < top_p <= acc_k (sampler.rs:238-245, the f32 fold).  Given keep,
+// the pick depends on u only through r0 = u * mass (sampler.rs:142-149), and
+// is nondecreasing in r0, so the r0 values that pick position j form one
+// interval of floats, found by bisection over their bit patterns.
+int or_reconcile(const float* logits, uint32_t usable, const tsm_row_params* prm,
+                 const uint32_t* recent, size_t nrecent, const uint32_t* mask, float u,
+                 uint32_t token, uint32_t keep, double* du, double* dp) {
+    Scratch s;
+    or_config cfg = cfg_from_params(*prm);
+    const float top_p = cfg.top_p;
+    const bool greedy = cfg.temperature <= 0.0f;
+    cfg.top_p = 1.0f;  // every survivor, with its probability
+    const size_t len = candidates(cfg, s, logits, usable, recent, nrecent, mask, nullptr);
+    *du = 0.0;
+    *dp = 0.0;
+    if (keep == 0 || keep > len) return 1;
+    if (greedy || top_p >= 1.0f) {
+        if (keep != len) return 1;
+    } else {
+        float total = 0.0f;
+        for (size_t j = 0; j < len; j++) total += s.probs[j];
+        float acc = 0.0f, lo = -INFINITY, hi = INFINITY;
+        for (size_t j = 0; j < len; j++) {
+            acc += s.probs[j] / total;
+            if (j + 1 == keep - 1) lo = acc;
+            if (j + 1 == keep) {
+                hi = keep == len ? INFINITY : acc;
+                break;
+            }
+        }
+        if (keep == 1) lo = -INFINITY;
+        // keep = k for top_p in (acc_{k-1}, acc_k]; for k = len, above acc_{len-1}
+        const double P = top_p;
+        if (P <= lo) *dp = static_cast<double>(lo) - P;
+        else if (P > hi) *dp = P - static_cast<double>(hi);
+    }
+    size_t j = 0;
+    while (j < keep && s.ri[j] != token) j++;
+    if (j == keep) return 1;
+    float mass = 0.0f;
+    for (size_t i = 0; i < keep; i++) mass += s.probs[i];
+    auto pick_at = [&](uint32_t bits) -> size_t {
+        float r;
+        std::memcpy(&r, &bits, 4);
+        for (size_t i = 0; i < keep; i++) {
+            r -= s.probs[i];
+            if (r <= 0.0f) return i;
+        }
+        return keep - 1;
+    };
+    const uint32_t top = 0x7F800000u;  // +inf: every finite r0 >= 0 lies below
+    // smallest r0 picking >= j, largest picking <= j
+    uint32_t a = 0, b = top;
+    while (a < b) {
+        const uint32_t m = a + (b - a) / 2;
+        if (pick_at(m) >= j) b = m;
+        else a = m + 1;
+    }
+    const uint32_t rlo = a;
+    a = 0;
+    b = top;
+    while (a < b) {
+        const uint32_t m = a + (b - a + 1) / 2;
+        if (pick_at(m) <= j) a = m;
+        else b = m - 1;
+    }
+    const uint32_t rhi = a;
+    if (pick_at(rlo) != j || pick_at(rhi) != j || rlo > rhi) return 1;
+    float flo, fhi;
+    std::memcpy(&flo, &rlo, 4);
+    std::memcpy(&fhi, &rhi, 4);
+    const double ulo = static_cast<double>(flo) / mass, uhi = static_cast<double>(fhi) / mass;
+    const double U = u;
+    if (U < ulo) *du = ulo - U;
+    else if (U > uhi) *du = U - uhi;
     return 0;
 }
 

@@ -48,23 +48,10 @@ typedef struct or_row_diag {
     uint32_t ranked;     /* |ranked| after truncation to want (A6)           */
     uint32_t survivors;  /* after min-p (== ranked when min-p is off)        */
     uint32_t keep;       /* kept by top-p (sequential f32, the reference)    */
-    uint32_t keep_exact; /* kept by top-p with exact (f64) partial sums      */
     uint32_t pick;       /* index of the pick in ranked order                */
-    uint32_t pick_exact; /* index the draw picks with exact (f64) sums       */
     uint32_t consumed_u; /* 1 if the row used its uniform                    */
-    double   u_gap;      /* distance of u from the nearest CDF boundary of
-                            the pick, in exact arithmetic (1 if no draw)     */
-    double   p_gap;      /* distance of top_p from the nearest exact
-                            cumulative around keep (1 if top-p is off)       */
-    double   mass64;     /* exact sum of the kept probabilities              */
     float    mass;       /* the reference's f32 mass                          */
     float    best;       /* ranked[0] penalized logit (l0)                   */
-    uint32_t token_exact; /* the pick with exact (f64) sums throughout: top-p
-                             keeps keep_exact, the draw spans their mass      */
-    double   ugap_exact; /* distance of u * mass from the CDF boundaries of
-                            that pick, relative to its mass (1 if no draw)   */
-    double   pgap_exact; /* distance of top_p from the exact cumulatives at
-                            keep_exact - 1 and keep_exact (1 if top-p off)    */
 } or_row_diag;
 
 /* ---- building blocks, each a restatement of one reference function ---- */
@@ -131,6 +118,18 @@ int or_sample_batch(const float* logits, uint32_t rows, uint32_t row_stride,
                     uint32_t* top_ids, float* top_lp, uint32_t top_stride,
                     float* prob, uint32_t* keep, or_row_diag* diag,
                     int nthreads);
+
+/*
+ * Parity diagnostics for one row (not a reference function): the distance
+ * *du that the row's uniform u, and *dp that its top_p, must move for the
+ * reference's arithmetic to pick `token` with kept count `keep` (0 when the
+ * pair is already the reference's).  `mask` is the row's packed mask or NULL.
+ * Returns 1 when no move of u and top_p gives the pair (the token is not
+ * among the first `keep` ranked ids, or `keep` is not a possible count).
+ */
+int or_reconcile(const float* logits, uint32_t usable, const tsm_row_params* p,
+                 const uint32_t* recent, size_t nrecent, const uint32_t* mask,
+                 float u, uint32_t token, uint32_t keep, double* du, double* dp);
 
 /* tsm_distribution() on host arrays.  Returns 0. */
 int or_distribution_batch(const float* logits, uint32_t rows,

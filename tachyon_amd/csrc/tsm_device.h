@@ -100,7 +100,9 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
 };
 
-__device__ __forceinline__ float glibc_expf(float x) {
+// The method with its 2^(i/32) table read through tab(i) (u64 bit patterns).
+template <class Tab>
+__device__ __forceinline__ float glibc_expf_core(float x, Tab tab) {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                          // |x| >= 88 or x is nan/inf
@@ -120,7 +122,7 @@ __device__ __forceinline__ float glibc_expf(float x) {
     const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
     kd -= shift;
     const double r = __builtin_fma(invln2n, xd, -kd);
-    uint64_t t = kExp2Tab[ki % 32];
+    uint64_t t = tab(static_cast<uint32_t>(ki % 32));
     t += ki << 47;
     const double s = __longlong_as_double(static_cast<long long>(t));
     const double zz = __builtin_fma(c0, r, c1);
@@ -129,6 +131,14 @@ __device__ __forceinline__ float glibc_expf(float x) {
     y = __builtin_fma(zz, r2, y);
     y = y * s;
     return static_cast<float>(y);
+}
+__device__ __forceinline__ float glibc_expf(float x) {
+    return glibc_expf_core(x, [](uint32_t i) { return kExp2Tab[i]; });
+}
+// The same with the table copied into LDS (a per-lane table index reads LDS
+// instead of issuing a memory load).
+__device__ __forceinline__ float glibc_expf_lds(float x, const uint64_t* tab) {
+    return glibc_expf_core(x, [tab](uint32_t i) { return tab[i]; });
 }
 
 // ---- LDS ----------------------------------------------------------------------
@@ -150,6 +160,16 @@ template <class T>
 __device__ __forceinline__ const TSM_GLOBAL_AS T* global_as(const T* p) {
     return (const TSM_GLOBAL_AS T*)p;
 }
+
+// A 16-byte load (one dwordx4) through a global-address-space pointer p,
+// 16-byte aligned.
+#ifndef TSM_HAVE_LOAD4
+typedef float tsm_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load4(const TSM_GLOBAL_AS float* p) {
+    const tsm_v4f v = *reinterpret_cast<const TSM_GLOBAL_AS tsm_v4f*>(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+#endif
 
 // Memory the kernel only reads, at addresses uniform over the workgroup (the
 // row's parameters, history offsets and uniform): loads through the constant

@@ -34,7 +34,7 @@
 // table are finished by re-reading the row (tsm_select.h), which is exact
 // and slower.
 #include "tsm_sample.h"
-#include "tsm_select.h"
+#include "tsm_nucleus.h"
 #include "tsm_split.h"
 
 namespace tsm {
@@ -926,6 +926,44 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in,
         if (!raw_ok) fin.need[SK_RAW] = 0;
         sel = buf_select(bufn, min(penn, kPenCap), true, fin);
     }
+    // raw top-n (sampler.rs:305-311), before the finish reuses the buffer's
+    // LDS: from the buffer's non-penalized entries and the penalized list, or
+    // by re-reading the row; thread i keeps the i-th composite
+    uint64_t raw_mine = ~0ull;
+    uint32_t nraw = 0;
+    if (nlp > 0) {
+        uint64_t* gcomp = f.gcomp();
+        if (raw_ok && sel.T[SK_RAW] != ~0ull) {
+            if (tid == 0) misc[M_CNT] = 0;
+            TSM_LDS_SYNC();
+            for (uint32_t i = tid; i < bufn; i += kBlock) {
+                const uint2 e = buf[i];
+                if (e.y & kEntPen) continue;
+                const uint64_t c = entry_comp(SK_ALL, e);
+                if (c <= sel.T[SK_RAW]) {
+                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
+                    if (pos < kExactCap) gcomp[pos] = c;
+                }
+            }
+            for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
+                const uint2 e = pen[i];
+                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y & kEntId);
+                if (c <= sel.T[SK_RAW]) {
+                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
+                    if (pos < kExactCap) gcomp[pos] = c;
+                }
+            }
+            TSM_LDS_SYNC();
+            const uint32_t g = min(misc[M_CNT], kExactCap);
+            TSM_LDS_SYNC();
+            sort_u64(gcomp, g);
+            nraw = min(g, nlp);
+        } else {
+            nraw = reread_raw_top(f, nlp);
+        }
+        if (tid < nraw) raw_mine = gcomp[tid];
+        TSM_LDS_SYNC();
+    }
     Pick pk;
     pk.token = 0;
     pk.keep = 0;
@@ -998,47 +1036,12 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in,
         if (a.out_keep) a.out_keep[row] = pk.keep;
         if (m.logprobs && a.out_logprob) a.out_logprob[row] = f.rowp[pk.token] - lse;
     }
-    if (nlp > 0) {
-        // raw top-n (sampler.rs:305-311): from the buffer's non-penalized
-        // entries and the penalized list, or by re-reading the row
-        uint64_t* gcomp = f.gcomp();
-        uint32_t nraw;
-        if (raw_ok && sel.T[SK_RAW] != ~0ull) {
-            if (tid == 0) misc[M_CNT] = 0;
-            TSM_LDS_SYNC();
-            for (uint32_t i = tid; i < bufn; i += kBlock) {
-                const uint2 e = buf[i];
-                if (e.y & kEntPen) continue;
-                const uint64_t c = entry_comp(SK_ALL, e);
-                if (c <= sel.T[SK_RAW]) {
-                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
-                    if (pos < kExactCap) gcomp[pos] = c;
-                }
-            }
-            for (uint32_t i = tid; i < min(penn, kPenCap); i += kBlock) {
-                const uint2 e = pen[i];
-                const uint64_t c = composite(canon_key(__uint_as_float(e.x)), e.y & kEntId);
-                if (c <= sel.T[SK_RAW]) {
-                    const uint32_t pos = atomicAdd(&misc[M_CNT], 1u);
-                    if (pos < kExactCap) gcomp[pos] = c;
-                }
-            }
-            TSM_LDS_SYNC();
-            const uint32_t g = min(misc[M_CNT], kExactCap);
-            TSM_LDS_SYNC();
-            sort_u64(gcomp, g);
-            nraw = min(g, nlp);
-        } else {
-            nraw = reread_raw_top(f, nlp);
-        }
-        if (tid < nraw) {
-            const uint64_t c = gcomp[tid];
-            const uint32_t id = static_cast<uint32_t>(c);
-            const float x = key_to_float(~static_cast<uint32_t>(c >> 32));
-            const size_t o = static_cast<size_t>(row) * a.top_stride + tid;
-            a.out_top_ids[o] = id;
-            if (a.out_top_lp) a.out_top_lp[o] = x - lse;
-        }
+    if (tid < nraw) {
+        const uint32_t id = static_cast<uint32_t>(raw_mine);
+        const float x = key_to_float(~static_cast<uint32_t>(raw_mine >> 32));
+        const size_t o = static_cast<size_t>(row) * a.top_stride + tid;
+        a.out_top_ids[o] = id;
+        if (a.out_top_lp) a.out_top_lp[o] = x - lse;
     }
 }
 

@@ -1,18 +1,14 @@
 // tsm_select.h - order statistics over one row for a 1024-thread workgroup:
 // the row re-read machinery (radix select in LDS over the row held in HBM /
-// L2 / MALL, mass selection for big nucleus sets) and the exact finish of a
-// ranked candidate list (the reference's sequential f32 arithmetic).
+// L2 / MALL) and the exact finish of a ranked candidate list (the reference's
+// sequential f32 arithmetic).
 //
-// A re-read streams the row in 16384-id tiles and answers order-statistic
-// questions with 11-bit LDS histograms:
-//   * select_kth: the k-th element in (value desc, id asc) order (radix);
-//   * mass selection: the first element whose cumulative probability reaches
-//     a target, with f64 partial sums, used when more than 1024 candidates
-//     remain.  Value bins (counts and masses per bin of (y0 - y) / t) find
-//     the bin that holds the target and one gather resolves it; radix rounds
-//     (mass_select) decide where a bin holds too many equal values.
-// When at most 1024 candidates remain they are gathered, sorted and finished
-// by exact_finalize, which reproduces the CPU sampler's roundings.
+// A re-read streams the row in 8192-id tiles and answers order-statistic
+// questions with 11-bit LDS histograms: select_kth gives the k-th element in
+// (value desc, id asc) order (radix).  When at most 1024 candidates remain
+// they are gathered, sorted and finished by exact_finalize, which reproduces
+// the CPU sampler's roundings; larger nucleus sets are finished by the value-
+// bin folds of tsm_nucleus.h.
 #pragma once
 
 #include "tsm_device.h"
@@ -25,7 +21,7 @@ namespace tsm {
 // the stream is done, the finish's ranked lists and the re-read's per-tile
 // history counts.  The histograms, the candidate buffer, the penalized list
 // and the scalars have their own regions.
-constexpr uint32_t kReTile = 16384;        // ids per tile of a re-read pass
+constexpr uint32_t kReTile = 8192;         // ids per tile of a re-read pass
 constexpr uint32_t kBitmapWords = 8192;    // history bitmap: rows of up to 262144 ids
 constexpr uint32_t kHashSlots = 4096;      // history count table (histories up to kHistFast ids)
 constexpr uint32_t kHistFast = kHashSlots / 2;
@@ -145,50 +141,83 @@ __device__ __forceinline__ bool keep_el(const Fin& f, const Filt& q, uint32_t id
     return true;
 }
 
-// One re-read of the row in tiles; fn(id, raw, penalized) for every id.  Each
-// thread loads G elements before it processes them, so G loads are in flight
-// per thread (G > 1 for the passes that dominate a long re-read path).
+// One re-read of the row in tiles of kReTile ids; fn(id, raw, penalized) for
+// every id.  The row is read as 16-byte blocks from the aligned address at or
+// below its start (ids outside the row are skipped; a block that reaches
+// before the row's first id or past its last is read element by element), two
+// blocks per thread per tile, with the next tile's blocks in flight while one
+// is processed.  Penalized rows count the history ids of each tile in LDS.
 template <int G = 1, class F>
 __device__ void row_pass(Fin& f, F&& fn) {
+    (void)G;
     const uint32_t tid = threadIdx.x;
     const uint32_t n = f.n;
     const bool penal = f.m.penal;
     const TSM_GLOBAL_AS float* rowp = global_as(f.rowp);
+    const uint32_t head = static_cast<uint32_t>((reinterpret_cast<uintptr_t>(f.rowp) >> 2) & 3u);
+    const TSM_GLOBAL_AS float* base = rowp - head;  // 16-byte aligned
+    const uint32_t span = head + n;         // aligned-base-relative end
+    const uint32_t nblk = (span + 3u) / 4u;  // blocks that hold row ids
+    const uint32_t full = span / 4u;         // blocks wholly before the row's end
+    constexpr uint32_t kTB = kReTile / 4u;  // blocks per tile
+    constexpr uint32_t kPer = kTB / kBlock;
+    static_assert(kPer * kBlock == kTB, "blocks per thread per tile");
     const TSM_GLOBAL_AS uint32_t* hist = global_as(f.hist);
     const uint32_t hc = min(f.hlen, TSM_MAX_HISTORY);
-    for (uint32_t tb = 0; tb < n; tb += kReTile) {
-        const uint32_t tl = min(kReTile, n - tb);
+    auto load_blk = [&](uint32_t j) -> float4 {
+        if (j < full && (j > 0u || head == 0u)) return load4(base + 4u * j);
+        float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (j < nblk) {
+            const uint32_t i0 = 4u * j;
+            if (i0 >= head && i0 < span) r.x = rowp[i0 - head];
+            if (i0 + 1u >= head && i0 + 1u < span) r.y = rowp[i0 + 1u - head];
+            if (i0 + 2u >= head && i0 + 2u < span) r.z = rowp[i0 + 2u - head];
+            if (i0 + 3u >= head && i0 + 3u < span) r.w = rowp[i0 + 3u - head];
+        }
+        return r;
+    };
+    float4 cur[kPer], nxt[kPer];
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; k++) cur[k] = load_blk(tid + k * kBlock);
+    const uint32_t ntiles = (nblk + kTB - 1u) / kTB;
+    for (uint32_t t = 0; t < ntiles; t++) {
+        if (t + 1u < ntiles) {
+#pragma unroll
+            for (uint32_t k = 0; k < kPer; k++) nxt[k] = load_blk((t + 1u) * kTB + tid + k * kBlock);
+        }
+        const uint32_t tb = t * kReTile;  // aligned-base-relative first id of the tile
         if (penal) {
             TSM_LDS_SYNC();
             for (uint32_t i = tid; i < kReTile / 2; i += kBlock) f.cnt()[i] = 0;
             TSM_LDS_SYNC();
             for (uint32_t h = tid; h < hc; h += kBlock) {
-                const uint32_t li = hist[h] - tb;
-                if (li < tl) atomicAdd(&f.cnt()[li >> 1], 1u << ((li & 1u) << 4));
+                const uint32_t li = hist[h] + head - tb;
+                if (li < kReTile && hist[h] < n) atomicAdd(&f.cnt()[li >> 1], 1u << ((li & 1u) << 4));
             }
             TSM_LDS_SYNC();
         }
-        for (uint32_t i0 = tid; i0 < tl; i0 += G * kBlock) {
-            float xs[G];
 #pragma unroll
-            for (int k = 0; k < G; k++) {
-                const uint32_t i = i0 + static_cast<uint32_t>(k) * kBlock;
-                xs[k] = i < tl ? rowp[tb + i] : 0.0f;
-            }
+        for (uint32_t k = 0; k < kPer; k++) {
+            const uint32_t j = t * kTB + tid + k * kBlock;
+            if (j >= nblk) continue;
+            const float xv[4] = {cur[k].x, cur[k].y, cur[k].z, cur[k].w};
 #pragma unroll
-            for (int k = 0; k < G; k++) {
-                const uint32_t i = i0 + static_cast<uint32_t>(k) * kBlock;
-                if (i < tl) {
-                    const uint32_t id = tb + i;
-                    const float x = xs[k];
-                    float y = x;
-                    if (penal) {
-                        const uint32_t c = (f.cnt()[i >> 1] >> ((i & 1u) << 4)) & 0xFFFFu;
-                        if (c) y = penalize(x, c, f.m, f.P);
-                    }
-                    fn(id, x, y);
+            for (uint32_t q = 0; q < 4u; q++) {
+                const uint32_t i = 4u * j + q;
+                if (i < head || i >= span) continue;
+                const float x = xv[q];
+                float y = x;
+                if (penal) {
+                    const uint32_t li = i - tb;
+                    const uint32_t c = (f.cnt()[li >> 1] >> ((li & 1u) << 4)) & 0xFFFFu;
+                    if (c) y = penalize(x, c, f.m, f.P);
                 }
+                fn(i - head, x, y);
             }
+        }
+        if (t + 1u < ntiles) {
+#pragma unroll
+            for (uint32_t k = 0; k < kPer; k++) cur[k] = nxt[k];
         }
     }
     TSM_LDS_SYNC();
@@ -273,8 +302,8 @@ __device__ __forceinline__ uint64_t select_kth(Fin& f, const Filt& q, uint32_t k
 }
 
 // The filtered element with the largest composite <= T, or ~0 when there is
-// none.  select_kth / mass_select return a threshold whose low bits may be
-// padding; this resolves it to the element itself (its id is the low word).
+// none.  select_kth returns a threshold whose low bits may be padding; this
+// resolves it to the element itself (its id is the low word).
 __device__ __forceinline__ uint64_t exact_at(Fin& f, const Filt& q, uint64_t T) {
     unsigned long long best = 0;
     uint32_t any = 0;
@@ -321,105 +350,6 @@ __device__ double block_excl_scan_f64(double v, double* tmp, double* total) {
     TSM_LDS_SYNC();
     *total = all;
     return before + inc - v;
-}
-
-struct MassSel {
-    uint64_t T;
-    double cum;     // cumulative probability through T
-    uint32_t rank;  // elements through T
-};
-
-// First filtered element, in (value desc, id asc) order, whose inclusive
-// cumulative p = exp((y - y0) / t) reaches `target`.
-__device__ __noinline__ MassSel mass_select(Fin& f_in, const Filt& q_in, float y0, double target) {
-    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
-    const Filt q = q_in;
-    const uint32_t tid = threadIdx.x;
-    uint64_t known = 0;
-    int known_lo = 64;
-    double cum_before = 0.0;
-    uint32_t cnt_before = 0;
-    double* dtmp = f.miscd() + 8;
-    for (int r = 0; r < 3; r++) {
-        const int lo = kRoundLo[r], w = kRoundW[r];
-        for (uint32_t i = tid; i < kBins; i += kBlock) {
-            f.hcnt()[i] = 0;
-            f.hmass()[i] = 0.0;
-        }
-        if (tid == 0) {
-            f.misc()[M_FIND] = 0xFFFFFFFFu;
-            f.misc()[M_FIND2] = 0;
-        }
-        TSM_LDS_SYNC();
-        const uint64_t kn = known;
-        const int kl = known_lo;
-        row_pass(f, [&](uint32_t id, float x, float y) {
-            const uint64_t c = comp_of(q.order, id, x, y);
-            if ((kl >= 64 || (c >> kl) == (kn >> kl)) && keep_el(f, q, id, y, c)) {
-                const uint32_t d = (c >> lo) & ((1u << w) - 1u);
-                atomicAdd(&f.hcnt()[d], 1u);
-                atomicAdd(&f.hmass()[d], static_cast<double>(glibc_expf((y - y0) / f.m.t)));
-            }
-        });
-        // thread t owns bins 2t, 2t+1
-        const uint32_t b0 = 2 * tid;
-        const uint32_t c0 = f.hcnt()[b0], c1 = f.hcnt()[b0 + 1];
-        const double m0 = f.hmass()[b0], m1 = f.hmass()[b0 + 1];
-        double mtot;
-        const double mb = block_excl_scan_f64(m0 + m1, dtmp, &mtot);
-        uint32_t ctot;
-        const uint32_t cb = block_excl_scan<kBlock>(c0 + c1, f.tmp(), &ctot);
-        const double base = cum_before + mb;
-        uint32_t cand = 0xFFFFFFFFu;
-        if (c0 > 0 && base + m0 >= target) cand = b0;
-        else if (c1 > 0 && base + m0 + m1 >= target) cand = b0 + 1;
-        if (cand != 0xFFFFFFFFu) atomicMin(&f.misc()[M_FIND], cand);
-        if (c0 + c1 > 0) atomicMax(&f.misc()[M_FIND2], (c1 > 0 ? b0 + 1 : b0) + 1);  // last nonempty + 1
-        TSM_LDS_SYNC();
-        uint32_t d = f.misc()[M_FIND];
-        const bool overshoot = d == 0xFFFFFFFFu;  // read now: select_from below rewrites M_FIND
-        if (overshoot) d = f.misc()[M_FIND2] - 1;   // target beyond the total: last element
-        if ((d >> 1) == tid) {
-            const bool second = d & 1u;
-            f.miscd()[0] = base + (second ? m0 : 0.0);
-            f.misc()[M_CNT] = cb + (second ? c0 : 0u);
-            f.misc()[M_TOTAL] = second ? c1 : c0;
-        }
-        TSM_LDS_SYNC();
-        cum_before = f.miscd()[0];
-        cnt_before += f.misc()[M_CNT];
-        const uint32_t ties = f.misc()[M_TOTAL];
-        known |= static_cast<uint64_t>(d) << lo;
-        known_lo = lo;
-        TSM_LDS_SYNC();
-        if (r == 2) {
-            // key resolved: all `ties` elements share one value and one p
-            const uint32_t key = ~static_cast<uint32_t>(known >> 32);
-            const float yk = key_to_float(key);
-            const double pk = static_cast<double>(glibc_expf((yk - y0) / f.m.t));
-            double need_d = pk > 0.0 ? ceil((target - cum_before) / pk) : 1.0;
-            uint32_t need = need_d < 1.0 ? 1u : (need_d > static_cast<double>(ties) ? ties : static_cast<uint32_t>(need_d));
-            if (overshoot) need = ties;  // take the last
-            MassSel s;
-            s.T = (need == ties) ? (known | 0xFFFFFFFFull) : select_from(f, q, need, 3, known, 32);
-            s.cum = cum_before + static_cast<double>(need) * pk;
-            s.rank = cnt_before + need;
-            return s;
-        }
-    }
-    return MassSel{};  // not reached
-}
-
-// Sum of p over the filtered elements (f64) and their count.
-__device__ __forceinline__ double mass_total(Fin& f, const Filt& q, float y0) {
-    double local = 0.0;
-    row_pass(f, [&](uint32_t id, float x, float y) {
-        const uint64_t c = comp_of(q.order, id, x, y);
-        if (keep_el(f, q, id, y, c)) local += static_cast<double>(glibc_expf((y - y0) / f.m.t));
-    });
-    double tot;
-    block_excl_scan_f64(local, f.miscd() + 8, &tot);
-    return tot;
 }
 
 // Gathers filtered elements' composites into gcomp (caller guarantees <= cap).
@@ -477,36 +407,12 @@ __device__ void sort_gathered(Fin& f, uint32_t n) {
     TSM_LDS_SYNC();
 }
 
-// Sorts a[0..n) ascending, n <= kBlock distinct values: each thread ranks
-// its value by counting the smaller ones (broadcast LDS reads, no barrier per
-// stage as in a bitonic sort) and stores it at its rank.
-__device__ __forceinline__ void rank_sort_u64(uint64_t* a, uint32_t n) {
-    const uint32_t tid = threadIdx.x;
-    uint64_t v = 0;
-    uint32_t r = 0;
-    if (tid < n) {
-        v = a[tid];
-        for (uint32_t j = 0; j < n; j++) r += a[j] < v ? 1u : 0u;
-    }
-    TSM_LDS_SYNC();
-    if (tid < n) a[r] = v;
-    TSM_LDS_SYNC();
-}
-
 constexpr int kNucGroup = 4;  // loads in flight per thread in the nucleus passes
 
-// ---- value-binned mass selection -------------------------------------------------
-// The nucleus of a row without top-k holds up to the whole vocabulary.  Its
-// mass selections (top-p, then the draw among the kept) bin the filtered
-// elements by value: bin(y) = floor((y0 - y) * mul), clamped to [0, kBins).
-// (y0 - y) * mul is monotone in y, so ascending bins visit the elements in
-// (value desc) order and equal values share a bin.  One pass builds the
-// counts and f64 masses p = exp((y - y0) / t) per bin; the bin where the
-// cumulative mass reaches the target is then gathered (at most kExactCap
-// elements), sorted, and resolved with an f64 prefix sum.  A bin with more
-// elements is split once more into kBins sub-bins by the fraction of
-// (y0 - y) * mul, which is exact for a non-clamped bin; a sub-bin that is
-// still too big (many equal values) is left to the radix selections.
+// ---- value bins ------------------------------------------------------------------
+// bin(y) = floor((y0 - y) * mul), clamped to [0, kBins): (y0 - y) * mul is
+// monotone in y, so ascending bins visit the elements in (value desc) order
+// and equal values share a bin.
 struct VBins {
     float y0, mul;
     __device__ __forceinline__ float pos(float y) const { return (y0 - y) * mul; }
@@ -514,223 +420,8 @@ struct VBins {
         const float d = pos(y);
         return d >= static_cast<float>(kBins - 1) ? kBins - 1u : (d > 0.0f ? static_cast<uint32_t>(d) : 0u);
     }
-    // level-2 index of y inside bin b < kBins - 1, where pos(y) - b in [0, 1) is exact
-    __device__ __forceinline__ uint32_t sub(float y, uint32_t b) const {
-        const float fr = (pos(y) - static_cast<float>(b)) * static_cast<float>(kBins);
-        return fr >= static_cast<float>(kBins - 1) ? kBins - 1u : (fr > 0.0f ? static_cast<uint32_t>(fr) : 0u);
-    }
 };
 static_assert(kBins == 2 * kBlock, "two bins per thread");
-
-// Counts and f64 masses of the filtered elements per bin (level 1), or per
-// sub-bin of bin b1 (level 2).  Returns false when a filtered value is NaN.
-__device__ __noinline__ bool vbin_hist(Fin& f_in, const Filt& q_in, const VBins& vb_in, bool level2, uint32_t b1) {
-    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
-    const Filt q = q_in;
-    const VBins vb = vb_in;
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t i = tid; i < kBins; i += kBlock) {
-        f.hcnt()[i] = 0;
-        f.hmass()[i] = 0.0;
-    }
-    if (tid == 0) f.misc()[M_VBAD] = 0;
-    TSM_LDS_SYNC();
-    // bin masses locate a target's bin and give the mass before it; they use
-    // the hardware exp2 (relative error of a term below 3e-6, largest for the
-    // smallest terms), while the elements of the bin that is resolved are
-    // summed from exact glibc_expf terms
-    const float l2t = 1.4426950408889634f / f.m.t;
-    uint32_t bad = 0;
-    row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
-        const uint64_t c = comp_of(q.order, id, x, y);
-        if (!keep_el(f, q, id, y, c)) return;
-        uint32_t b = vb.bin(y);
-        if (level2) {
-            if (b != b1) return;
-            b = vb.sub(y, b1);
-        }
-        bad |= y != y;
-        atomicAdd(&f.hcnt()[b], 1u);
-        atomicAdd(&f.hmass()[b], static_cast<double>(__builtin_amdgcn_exp2f((y - vb.y0) * l2t)));
-    });
-    if (bad) f.misc()[M_VBAD] = 1u;
-    TSM_LDS_SYNC();
-    const bool ok = f.misc()[M_VBAD] == 0;
-    TSM_LDS_SYNC();
-    return ok;
-}
-
-// Element count and f64 mass of the histogram.
-__device__ __forceinline__ uint32_t vbin_totals(Fin& f, double* mass) {
-    const uint32_t b0 = 2 * threadIdx.x;
-    block_excl_scan_f64(f.hmass()[b0] + f.hmass()[b0 + 1], f.miscd() + 8, mass);
-    return block_sum<kBlock>(f.hcnt()[b0] + f.hcnt()[b0 + 1], f.tmp());
-}
-
-struct BinHit {
-    uint32_t bin;       // kBins: the histogram is empty
-    uint32_t cnt;       // elements in the bin
-    uint32_t before_n;  // elements in earlier bins
-    double before;      // base + the mass of earlier bins
-};
-
-// The first non-empty bin whose cumulative mass (from base) reaches target,
-// or the last non-empty bin when none does.
-__device__ __forceinline__ BinHit vbin_find(Fin& f, double base, double target) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t b0 = 2 * tid;
-    const uint32_t c0 = f.hcnt()[b0], c1 = f.hcnt()[b0 + 1];
-    const double m0 = f.hmass()[b0], m1 = f.hmass()[b0 + 1];
-    if (tid == 0) {
-        f.misc()[M_FIND] = 0xFFFFFFFFu;
-        f.misc()[M_FIND2] = 0;
-    }
-    double mtot;
-    const double mb = block_excl_scan_f64(m0 + m1, f.miscd() + 8, &mtot);  // barriers order the init above
-    uint32_t ctot;
-    const uint32_t cb = block_excl_scan<kBlock>(c0 + c1, f.tmp(), &ctot);
-    const double bs = base + mb;
-    uint32_t cand = 0xFFFFFFFFu;
-    if (c0 > 0 && bs + m0 >= target) cand = b0;
-    else if (c1 > 0 && bs + m0 + m1 >= target) cand = b0 + 1;
-    if (cand != 0xFFFFFFFFu) atomicMin(&f.misc()[M_FIND], cand);
-    if (c0 + c1 > 0) atomicMax(&f.misc()[M_FIND2], (c1 > 0 ? b0 + 1 : b0) + 1);
-    TSM_LDS_SYNC();
-    uint32_t d = f.misc()[M_FIND];
-    if (d == 0xFFFFFFFFu) d = f.misc()[M_FIND2] == 0 ? kBins : f.misc()[M_FIND2] - 1;
-    if (d < kBins && (d >> 1) == tid) {
-        const bool second = d & 1u;
-        f.miscd()[0] = bs + (second ? m0 : 0.0);
-        f.misc()[M_CNT] = cb + (second ? c0 : 0u);
-        f.misc()[M_TOTAL] = second ? c1 : c0;
-    }
-    TSM_LDS_SYNC();
-    BinHit h;
-    h.bin = d;
-    h.cnt = d < kBins ? f.misc()[M_TOTAL] : 0u;
-    h.before_n = d < kBins ? f.misc()[M_CNT] : ctot;
-    h.before = d < kBins ? f.miscd()[0] : base + mtot;
-    TSM_LDS_SYNC();
-    return h;
-}
-
-// vbin_find for two targets (from base 0) with one scan of the bins.
-__device__ __forceinline__ void vbin_find2(Fin& f, double ta, double tb, BinHit* ha, BinHit* hb) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t b0 = 2 * tid;
-    const uint32_t c0 = f.hcnt()[b0], c1 = f.hcnt()[b0 + 1];
-    const double m0 = f.hmass()[b0], m1 = f.hmass()[b0 + 1];
-    uint32_t* fs = f.misc() + M_RED;  // first hits [0..1], last non-empty + 1 [2], per target: before_n, cnt
-    if (tid == 0) {
-        fs[0] = fs[1] = 0xFFFFFFFFu;
-        fs[2] = 0;
-    }
-    double mtot;
-    const double bs = block_excl_scan_f64(m0 + m1, f.miscd() + 8, &mtot);  // barriers order the init above
-    uint32_t ctot;
-    const uint32_t cb = block_excl_scan<kBlock>(c0 + c1, f.tmp(), &ctot);
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const double target = k == 0 ? ta : tb;
-        uint32_t cand = 0xFFFFFFFFu;
-        if (c0 > 0 && bs + m0 >= target) cand = b0;
-        else if (c1 > 0 && bs + m0 + m1 >= target) cand = b0 + 1;
-        if (cand != 0xFFFFFFFFu) atomicMin(&fs[k], cand);
-    }
-    if (c0 + c1 > 0) atomicMax(&fs[2], (c1 > 0 ? b0 + 1 : b0) + 1);
-    TSM_LDS_SYNC();
-    uint32_t d[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        d[k] = fs[k];
-        if (d[k] == 0xFFFFFFFFu) d[k] = fs[2] == 0 ? kBins : fs[2] - 1;
-        if (d[k] < kBins && (d[k] >> 1) == tid) {
-            const bool second = d[k] & 1u;
-            f.miscd()[k] = bs + (second ? m0 : 0.0);
-            fs[3 + k] = cb + (second ? c0 : 0u);
-            fs[5 + k] = second ? c1 : c0;
-        }
-    }
-    TSM_LDS_SYNC();
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        BinHit* h = k == 0 ? ha : hb;
-        h->bin = d[k];
-        h->cnt = d[k] < kBins ? fs[5 + k] : 0u;
-        h->before_n = d[k] < kBins ? fs[3 + k] : ctot;
-        h->before = d[k] < kBins ? f.miscd()[k] : mtot;
-    }
-    TSM_LDS_SYNC();
-}
-
-// Gathers the filtered elements of bin b1 (level 1) or of its sub-bin b2
-// (level 2), sorts them, and returns the first whose cumulative mass (from
-// h.before) reaches target, or the last.  False when the bin holds more than
-// kExactCap elements.
-__device__ __forceinline__ bool vbin_resolve(Fin& f, const Filt& q, const VBins& vb, bool level2, uint32_t b1, const BinHit& h,
-                             uint32_t before_n, double target, MassSel* out) {
-    const uint32_t tid = threadIdx.x;
-    if (h.bin >= kBins || h.cnt == 0 || h.cnt > kExactCap) return false;
-    const uint32_t b2 = h.bin;
-    if (tid == 0) f.misc()[M_CNT] = 0;
-    TSM_LDS_SYNC();
-    row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
-        const uint64_t c = comp_of(q.order, id, x, y);
-        if (!keep_el(f, q, id, y, c)) return;
-        const uint32_t b = vb.bin(y);
-        if (b != b1 || (level2 && vb.sub(y, b1) != b2)) return;
-        const uint32_t pos = atomicAdd(&f.misc()[M_CNT], 1u);
-        if (pos < kExactCap) f.gcomp()[pos] = c;
-    });
-    const uint32_t n = min(f.misc()[M_CNT], kExactCap);
-    TSM_LDS_SYNC();
-    if (n == 0) return false;
-    rank_sort_u64(f.gcomp(), n);
-    TSM_LDS_SYNC();
-    double p = 0.0;
-    uint64_t c = 0;
-    if (tid < n) {
-        c = f.gcomp()[tid];
-        const float y = key_to_float(~static_cast<uint32_t>(c >> 32));
-        p = static_cast<double>(glibc_expf((y - vb.y0) / f.m.t));
-    }
-    if (tid == 0) f.misc()[M_FIND] = 0xFFFFFFFFu;
-    double tot;
-    const double incl = h.before + (block_excl_scan_f64(p, f.miscd() + 8, &tot) + p);
-    if (tid < n && incl >= target) atomicMin(&f.misc()[M_FIND], tid);
-    TSM_LDS_SYNC();
-    uint32_t j = f.misc()[M_FIND];
-    if (j == 0xFFFFFFFFu) j = n - 1;
-    if (tid == j) {
-        f.miscd()[0] = incl;
-        f.gcomp()[kExactCap - 1] = c;  // sorted list no longer needed
-    }
-    TSM_LDS_SYNC();
-    out->T = f.gcomp()[kExactCap - 1];
-    out->cum = f.miscd()[0];
-    out->rank = before_n + j + 1;
-    TSM_LDS_SYNC();
-    return true;
-}
-
-// mass selection over the histogram in LDS (level 1 bins of q): the element
-// of q whose cumulative mass reaches target.  *l1 is cleared when the level-1
-// histogram was overwritten.  False when the radix selection must decide.
-__device__ __noinline__ bool vbin_select(Fin& f_in, const Filt& q_in, const VBins& vb_in, double target, MassSel* out,
-                                         BinHit* hit, bool* l1) {
-    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
-    const Filt q = q_in;
-    const VBins vb = vb_in;
-    const BinHit h = vbin_find(f, 0.0, target);
-    *hit = h;
-    if (h.bin >= kBins) return false;
-    if (h.cnt <= kExactCap) return vbin_resolve(f, q, vb, false, h.bin, h, h.before_n, target, out);
-    if (h.bin >= kBins - 1) return false;  // clamped bin: no exact split
-    *l1 = false;
-    if (!vbin_hist(f, q, vb, true, h.bin)) return false;
-    const BinHit h2 = vbin_find(f, h.before, target);
-    return vbin_resolve(f, q, vb, true, h.bin, h2, h.before_n + h2.before_n, target, out);
-}
 
 struct Pick {
     uint32_t token, keep;
@@ -927,109 +618,6 @@ __device__ uint32_t reread_topk_list(Fin& f, uint32_t nallow) {
     return len;
 }
 
-// Top-p and the draw from one gather.  The kept mass M lies in (before,
-// before + mass] of the top-p bin hp, so the draw target u * M can only fall
-// in the bins that cover [u * before, u * (before + mass)]: hp and those bins
-// are gathered together, sorted, and both picks are resolved from the list
-// with f64 prefix sums.  False (nothing decided, the histogram intact) when
-// they hold more than kExactCap elements; the caller then selects in passes
-// of their own.
-__device__ __noinline__ bool vbin_topp_draw(Fin& f_in, const Filt& q_in, const VBins& vb_in, double target_p,
-                                            float u, MassSel* sp, uint64_t* drawn) {
-    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
-    const Filt q = q_in;
-    const VBins vb = vb_in;
-    const uint32_t tid = threadIdx.x;
-    const BinHit hp = vbin_find(f, 0.0, target_p);
-    if (hp.bin >= kBins || hp.cnt == 0 || hp.cnt > kExactCap) return false;
-    const double hmass_p = f.hmass()[hp.bin];
-    const double du = static_cast<double>(u);
-    BinHit hlo, hhi;
-    vbin_find2(f, du * hp.before, du * (hp.before + hmass_p), &hlo, &hhi);
-    const uint32_t jlo = min(hlo.bin, hp.bin), jhi = min(hhi.bin, hp.bin);
-    // bins jlo..jhi (contiguous) and hp.bin; hp's elements sort last
-    const uint32_t n_low = jhi < hp.bin ? (hhi.before_n + hhi.cnt) - hlo.before_n : hp.before_n - hlo.before_n;
-    const uint32_t want_n = n_low + hp.cnt;
-    if (want_n > kExactCap) return false;
-    if (tid == 0) f.misc()[M_CNT] = 0;
-    TSM_LDS_SYNC();
-    const uint32_t bstar = hp.bin;
-    row_pass<kNucGroup>(f, [&](uint32_t id, float x, float y) {
-        const uint64_t c = comp_of(q.order, id, x, y);
-        if (!keep_el(f, q, id, y, c)) return;
-        const uint32_t b = vb.bin(y);
-        if (b != bstar && (b < jlo || b > jhi)) return;
-        const uint32_t pos = atomicAdd(&f.misc()[M_CNT], 1u);
-        if (pos < kExactCap) f.gcomp()[pos] = c;
-    });
-    const uint32_t n = f.misc()[M_CNT];
-    TSM_LDS_SYNC();
-    if (n != want_n) return false;  // not reached: the histogram counted the same elements
-    rank_sort_u64(f.gcomp(), n);
-    TSM_LDS_SYNC();
-    const uint32_t s0 = n - hp.cnt;  // list index of hp's first element
-    double p = 0.0;
-    uint64_t c = 0;
-    if (tid < n) {
-        c = f.gcomp()[tid];
-        const float y = key_to_float(~static_cast<uint32_t>(c >> 32));
-        p = static_cast<double>(glibc_expf((y - vb.y0) / f.m.t));
-    }
-    // top-p inside hp
-    if (tid == 0) {
-        f.misc()[M_FIND] = 0xFFFFFFFFu;
-        f.misc()[M_FIND2] = 0xFFFFFFFFu;
-    }
-    double tot;
-    const double pin = tid >= s0 ? p : 0.0;
-    const double cum_p = hp.before + (block_excl_scan_f64(pin, f.miscd() + 8, &tot) + pin);
-    if (tid >= s0 && tid < n && cum_p >= target_p) atomicMin(&f.misc()[M_FIND], tid);
-    TSM_LDS_SYNC();
-    uint32_t jp = f.misc()[M_FIND];
-    if (jp == 0xFFFFFFFFu) jp = n - 1;
-    if (tid == jp) f.miscd()[0] = cum_p;
-    TSM_LDS_SYNC();
-    const double M = f.miscd()[0];
-    const double td = du * M;
-    // the draw: inside hp (through the top-p pick) or in bins jlo..jhi; with
-    // no bin gathered below hp, hp holds the row's first elements
-    const bool in_hp = td > hp.before || s0 == 0;
-    const double plo = (!in_hp && tid < s0) ? p : 0.0;
-    const double cum_d = in_hp ? cum_p : hlo.before + (block_excl_scan_f64(plo, f.miscd() + 8, &tot) + plo);
-    const uint32_t lo_j = in_hp ? s0 : 0u, hi_j = in_hp ? jp + 1 : s0;
-    if (tid >= lo_j && tid < hi_j && cum_d >= td) atomicMin(&f.misc()[M_FIND2], tid);
-    TSM_LDS_SYNC();
-    uint32_t jd = f.misc()[M_FIND2];
-    bool ok = true;
-    if (jd == 0xFFFFFFFFu) {
-        if (in_hp) jd = jp;  // u * M reaches past the pick only by rounding: the last kept
-        else ok = false;     // rounding put the target outside the gathered bins
-    }
-    TSM_LDS_SYNC();
-    if (!ok) return false;
-    sp->T = f.gcomp()[jp];
-    sp->cum = M;
-    sp->rank = hp.before_n + (jp - s0) + 1;
-    *drawn = f.gcomp()[jd];
-    TSM_LDS_SYNC();
-    return true;
-}
-
-// Restricts the level-1 histogram to the elements through the top-p pick,
-// which lies in bin hb: later bins are emptied and bin hb keeps its kept part.
-__device__ __forceinline__ void vbin_cut(Fin& f, const BinHit& hb, uint32_t keep, double mass) {
-    for (uint32_t i = threadIdx.x; i < kBins; i += kBlock) {
-        if (i > hb.bin) {
-            f.hcnt()[i] = 0;
-            f.hmass()[i] = 0.0;
-        } else if (i == hb.bin) {
-            f.hcnt()[i] = keep - hb.before_n;
-            f.hmass()[i] = mass - hb.before;
-        }
-    }
-    TSM_LDS_SYNC();
-}
-
 // Up to kExactCap survivors: gathered, sorted and finished exactly.
 __device__ __noinline__ Pick nucleus_exact(Fin& f_in, const Filt& q_in, float u, const DistOut* dist) {
     Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
@@ -1037,193 +625,6 @@ __device__ __noinline__ Pick nucleus_exact(Fin& f_in, const Filt& q_in, float u,
     const uint32_t g = gather_pass<kNucGroup>(f, q, kExactCap);
     sort_gathered(f, g);
     return finish_list(f, g, u, dist);
-}
-
-// Rows without top-k (window > 1024): the cutoff set (sampler.rs:195-208),
-// the window rule, truncation to want, min-p, then top-p and the draw, all
-// by re-reading the row.  Up to 1024 survivors are finished exactly
-// (finish_list); larger sets use f64 mass selections, through value bins
-// where they resolve and through radix rounds otherwise.
-__device__ __noinline__ Pick reread_nucleus(Fin& f, uint32_t nallow, float u, const DistOut* dist) {
-    const uint32_t tid = threadIdx.x;
-    const RowMode& m = f.m;
-    float mall = -INFINITY, mal = -INFINITY, mlo = INFINITY;
-    {
-        float la = -INFINITY, lb = -INFINITY, lc = INFINITY;
-        row_pass<2 * kNucGroup>(f, [&](uint32_t id, float x, float y) {
-            la = fmaxf(la, y);
-            lc = fminf(lc, y);
-            if (m.constrained && allowed_bit(f, id)) lb = fmaxf(lb, y);
-        });
-        la = wave_max(la);
-        lb = wave_max(lb);
-        lc = -wave_max(-lc);
-        float* ftmp = reinterpret_cast<float*>(f.miscd() + 8);
-        if ((tid & 63) == 0) {
-            ftmp[tid / 64] = la;
-            ftmp[16 + tid / 64] = lb;
-            ftmp[32 + tid / 64] = lc;
-        }
-        TSM_LDS_SYNC();
-        for (int w = 0; w < kBlock / kWave; w++) {
-            mall = fmaxf(mall, ftmp[w]);
-            mal = fmaxf(mal, ftmp[16 + w]);
-            mlo = fminf(mlo, ftmp[32 + w]);
-        }
-        TSM_LDS_SYNC();
-    }
-    const float cut = mall - 30.0f * m.t;  // sampler.rs:198-199
-    const float y0 = m.constrained ? mal : mall;
-    // value bins over [y0 - 30.5 t, y0], or the row's narrower range
-    VBins vb;
-    vb.y0 = y0;
-    {
-        float span = fminf(30.5f, (y0 - mlo) / m.t);
-        if (!(span > 0.0f)) span = 1.0f;
-        vb.mul = (static_cast<float>(kBins) / span) / m.t;
-    }
-    bool use_vb = m.t > 0.0f && __builtin_isfinite(y0) && __builtin_isfinite(vb.mul) && vb.mul > 0.0f;
-    bool hist_ok = false;  // the level-1 histogram in LDS is that of q2
-    Filt q0;
-    q0.order = ORD_TOTAL_Y;
-    q0.use_cut = true;
-    q0.cut = cut;
-    q0.need_allowed = m.constrained;
-    uint32_t n0;
-    if (f.P.min_p > 0.0f && !m.constrained && m.want >= f.n) {
-        // the cutoff set's size decides nothing here (no truncation, no
-        // fallback): min-p's count below is the first one needed
-        n0 = m.want;
-    } else if (use_vb) {
-        use_vb = vbin_hist(f, q0, vb, false, 0);
-        double mass0;
-        n0 = vbin_totals(f, &mass0);
-        hist_ok = use_vb;
-    } else {
-        n0 = count_pass<kNucGroup>(f, q0);
-    }
-    if (m.constrained && n0 == 0) {  // sampler.rs:211-221
-        q0.use_cut = false;
-        n0 = nallow;
-        hist_ok = false;
-    }
-    Filt q1 = q0;
-    uint32_t n1 = n0;
-    if (n0 > m.want) {  // ranked.truncate(want)
-        q1.use_max = true;
-        q1.max_comp = select_kth(f, q0, m.want);
-        n1 = m.want;
-        hist_ok = false;
-    }
-    Filt q2 = q1;
-    uint32_t n2c = n1;
-    if (f.P.min_p > 0.0f) {  // extension: min-p prefix
-        q2.use_minp = true;
-        q2.y0 = y0;
-        q2.minp = f.P.min_p;
-        // p >= min_p  <=>  y >= y0 + t ln(min_p), up to the roundings of the
-        // subtraction, the division and expf (below 1e-6 relative): a band of
-        // 1e-3 (|y0| + |t ln min_p| + t) on either side holds every value
-        // those roundings could put on the other side
-        const float a = m.t * logf(f.P.min_p);
-        const float band = 1e-3f * (fabsf(y0) + fabsf(a) + m.t);
-        q2.minp_lo = (y0 + a) - band;
-        q2.minp_hi = (y0 + a) + band;
-        n2c = count_pass<kNucGroup>(f, q2);
-        if (n2c == 0) {
-            q2 = q1;
-            q2.use_max = true;
-            q2.max_comp = select_kth(f, q1, 1);
-            n2c = 1;
-        }
-        hist_ok = false;
-    }
-    if (n2c <= kExactCap) return nucleus_exact(f, q2, u, dist);
-    // more than 1024 candidates: exact-arithmetic (f64) cumulative sums
-    double total;
-    if (use_vb && !hist_ok) {
-        use_vb = vbin_hist(f, q2, vb, false, 0);
-        hist_ok = use_vb;
-    }
-    if (hist_ok) vbin_totals(f, &total);
-    else total = mass_total(f, q2, y0);
-    Filt q3 = q2;
-    double mass = total;
-    uint32_t keep = n2c;
-    BinHit hp;
-    hp.bin = kBins;
-    if (!(f.P.top_p >= 1.0f) && !dist && hist_ok) {
-        // top-p and the draw from one gather
-        const double target = static_cast<double>(f.P.top_p) * total;
-        MassSel sp;
-        uint64_t ce;
-        if (vbin_topp_draw(f, q2, vb, target, u, &sp, &ce)) {
-            Pick pk;
-            pk.keep = sp.rank;
-            pk.mass = static_cast<float>(sp.cum);
-            const float yk = key_to_float(~static_cast<uint32_t>(ce >> 32));
-            pk.token = static_cast<uint32_t>(ce);
-            pk.prob = static_cast<float>(static_cast<double>(glibc_expf((yk - y0) / m.t)) / sp.cum);
-            return pk;
-        }
-    }
-    if (!(f.P.top_p >= 1.0f)) {
-        const double target = static_cast<double>(f.P.top_p) * total;
-        MassSel sp;
-        if (!(hist_ok && vbin_select(f, q2, vb, target, &sp, &hp, &hist_ok))) {
-            hist_ok = false;
-            sp = mass_select(f, q2, y0, target);
-        }
-        q3.use_max = true;
-        q3.max_comp = sp.T;
-        mass = sp.cum;
-        keep = sp.rank;
-    }
-    Pick pk;
-    pk.keep = keep;
-    pk.mass = static_cast<float>(mass);
-    if (dist) {
-        Filt qd = q3;
-        const uint32_t k = min(min(keep, dist->stride), kExactCap);
-        if (k < keep) {
-            qd.use_max = true;
-            qd.max_comp = select_kth(f, q3, k);
-        }
-        const uint32_t g = gather_pass(f, qd, kExactCap);
-        sort_gathered(f, g);
-        for (uint32_t j = tid; j < g; j += kBlock) {
-            dist->ids[j] = f.rid()[j];
-            dist->probs[j] = static_cast<float>(static_cast<double>(glibc_expf((f.ry()[j] - y0) / m.t)) / mass);
-        }
-        if (keep > g && tid == 0) atomicOr(dist->status, TSM_STATUS_DIST_TRUNCATED);
-        pk.token = g > 0 ? f.rid()[0] : 0u;
-        pk.prob = 0.0f;
-        TSM_LDS_SYNC();
-        return pk;
-    }
-    // the draw among the kept (sampler.rs:142-150)
-    const double dtarget = static_cast<double>(u) * mass;
-    uint64_t ce;
-    bool drawn = false;
-    if (use_vb) {
-        if (hist_ok && hp.bin < kBins) vbin_cut(f, hp, keep, mass);
-        if (!hist_ok) hist_ok = vbin_hist(f, q3, vb, false, 0);
-        MassSel sd;
-        BinHit hd;
-        bool l1 = true;
-        if (hist_ok && vbin_select(f, q3, vb, dtarget, &sd, &hd, &l1)) {
-            ce = sd.T;
-            drawn = true;
-        }
-    }
-    if (!drawn) {
-        const MassSel sr = mass_select(f, q3, y0, dtarget);
-        ce = exact_at(f, q3, sr.T);
-    }
-    const float yk = key_to_float(~static_cast<uint32_t>(ce >> 32));
-    pk.token = static_cast<uint32_t>(ce);
-    pk.prob = static_cast<float>(static_cast<double>(glibc_expf((yk - y0) / m.t)) / mass);
-    return pk;
 }
 
 // Raw top-n (value desc, id asc) by re-reading the row: composites of the

@@ -44,6 +44,7 @@
 #define HIP_SYMBOL(x) (&(x))
 #define TSM_GLOBAL_AS
 #define TSM_CONST_AS  // the host has one address space
+#define TSM_HAVE_LOAD4
 
 struct dim3 {
     uint32_t x, y, z;
@@ -57,6 +58,7 @@ struct alignas(16) uint4 { uint32_t x, y, z, w; };
 inline uint2 make_uint2(uint32_t x, uint32_t y) { return uint2{x, y}; }
 inline uint4 make_uint4(uint32_t x, uint32_t y, uint32_t z, uint32_t w) { return uint4{x, y, z, w}; }
 inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
+inline float4 load4(const float* p) { return float4{p[0], p[1], p[2], p[3]}; }
 
 namespace emu {
 #ifdef EMU_THREADS

@@ -56,9 +56,8 @@ def run_case(ctx, w, label, nthreads=16):
     got = run_workload(ctx, w)
     assert ctx.status() == 0
     ref = pyoracle.sample_batch(w, nthreads=nthreads)
-    exact_rows, exempt, exact_picks = check(w, got, ref, label)
-    say(f"[gpu] {label}: ok, exact rows {exact_rows}/{w.rows}, boundary-exempt {exempt}, "
-        f"nucleus picks equal to exact arithmetic {exact_picks}")
+    exact_rows, boundary = check(w, got, ref, label)
+    say(f"[gpu] {label}: ok, bit-exact rows {exact_rows}/{w.rows}, within the measured 1e-5 boundary {boundary}")
     return got, ref
 
 
@@ -135,9 +134,9 @@ def test_parity_split_path(ctx, name, kinds):
     got = run_workload(ctx, w, kinds=kinds)
     assert ctx.status() == 0
     ref = pyoracle.sample_batch(w, nthreads=16)
-    exact_rows, exempt, _ = check(w, got, ref, f"split {name}")
+    exact_rows, boundary = check(w, got, ref, f"split {name}")
     check_mask_property(w, got)
-    say(f"[gpu] split path {name}: ok, exact rows {exact_rows}/{w.rows}, boundary-exempt {exempt}")
+    say(f"[gpu] split path {name}: ok, bit-exact rows {exact_rows}/{w.rows}, within the boundary {boundary}")
 
 
 def test_split_path_row_kind_mismatch(ctx):

@@ -310,3 +310,107 @@ def test_constrained_window_rule_differs_from_mask_then_topk(oracle):
     w.mask = wl.pack_mask(allowed)
     r = oracle.sample_batch(w)
     assert r.diag["path"][0] == 3 and r.keep[0] == 3 and r.token[0] in (600, 601, 602)
+
+
+# ---- the measured boundary check (or_reconcile) -------------------------------
+
+def _reference_pick(w, r, u, top_p=None):
+    """The reference's (token, keep) for row r with its uniform set to u (and
+    top_p, if given): the oracle run on a one-row copy."""
+    from oracle import pyoracle
+
+    one = wl.Workload("one", w.logits[r:r + 1].copy(), w.usable, w.params[r:r + 1].copy(), None, None, None,
+                      np.array([u], np.float32))
+    if top_p is not None:
+        one.params["top_p"][0] = top_p
+    if w.hist_ids is not None:
+        a, b = int(w.hist_offsets[r]), int(w.hist_offsets[r + 1])
+        one.hist_ids = w.hist_ids[a:b].copy()
+        one.hist_offsets = np.array([0, b - a], np.uint32)
+    res = pyoracle.sample_batch(one)
+    return int(res.token[0]), int(res.keep[0])
+
+
+def test_reconcile_matches_a_scan_of_u(oracle):
+    """or_reconcile's u-shift against brute force: u swept over a grid of
+    2^-16 steps, each value run through the reference's arithmetic; the
+    nearest u that returns a given token must lie within one grid step of
+    u + du (or u - du)."""
+    from oracle import pyoracle
+
+    w = wl.random_case(seed=61, vocab=1500, rows=4, mode="nucleus", logprobs=False, hist_len=0)
+    grid = np.arange(0, 1 << 16, dtype=np.float64) / (1 << 16)
+    for r in range(w.rows):
+        u0 = float(w.uniforms[r])
+        _, keep = _reference_pick(w, r, u0)
+        picks = {}
+        for u in grid[::64]:
+            t, k = _reference_pick(w, r, np.float32(u))
+            picks.setdefault(t, []).append(u)
+        for tok, us in list(picks.items())[:6]:
+            du, dp = pyoracle.reconcile(w, r, tok, keep)
+            assert dp == 0.0
+            nearest = min(abs(u - u0) for u in us)
+            # the scan sees the token's interval only at its grid points
+            assert du <= nearest + 1e-12, (r, tok, du, nearest)
+            assert nearest - du <= 64.0 / (1 << 16), (r, tok, du, nearest)
+            # and the reference returns the token at the reconciled u
+            if du > 0.0:
+                side = 1.0 if min(us, key=lambda u: abs(u - u0)) > u0 else -1.0
+                u1 = np.float32(u0 + side * (du + 1e-7))
+                assert _reference_pick(w, r, u1)[0] == tok, (r, tok, du)
+
+
+def test_reconcile_top_p_shift(oracle):
+    """The kept count as a step function of top_p: a kept count one off the
+    reference's needs the measured shift in top_p, and the reference returns
+    that count once top_p moves by it."""
+    from oracle import pyoracle
+
+    w = wl.random_case(seed=62, vocab=1500, rows=4, mode="topp", logprobs=False, hist_len=0)
+    for r in range(w.rows):
+        tok, keep = _reference_pick(w, r, float(w.uniforms[r]))
+        assert pyoracle.reconcile(w, r, tok, keep) == (0.0, 0.0)
+        if keep < 3:
+            continue
+        k2 = keep - 1
+        res = pyoracle.reconcile(w, r, pyoracle.sample_batch(w).token[r], k2)
+        if res is None:  # the token lies beyond k2: a pair no move reaches
+            continue
+        du, dp = res
+        assert dp > 0.0
+        p1 = np.float32(float(w.params["top_p"][r]) - dp)
+        assert _reference_pick(w, r, float(w.uniforms[r]), top_p=p1)[1] == k2, (r, dp)
+
+
+def test_boundary_check_rejects_exact_arithmetic_picks(oracle):
+    """The parity bar measures the boundary: picks made with exact (f64)
+    sums, as an earlier device path made them on c2's temperature-only rows,
+    differ from the reference's sequential f32 folds by more than the 1e-5
+    the north star allows on rows 8-10, 12, 13 and 15; the check rejects
+    them.  The f64 view here is computed independently of the oracle's
+    sampler (numpy sort, math.fsum mass, f64 cumulative sums)."""
+    from oracle import pyoracle
+    from parity import TOL_U, boundary_shift
+
+    w = wl.c2()
+    ref = pyoracle.sample_batch(w)
+    over = []
+    for r in range(8, 16):
+        p = w.params[r]
+        h = w.hist_ids[w.hist_offsets[r]:w.hist_offsets[r + 1]]
+        y = pyoracle.penalize(w.logits[r, :w.usable], h, float(p["repetition_penalty"]),
+                              float(p["presence_penalty"]), float(p["frequency_penalty"]))
+        t = np.float32(p["temperature"])
+        cut = np.float32(y.max() - np.float32(30.0) * t)
+        ids = np.nonzero(y >= cut)[0]
+        ids = ids[np.lexsort((ids, -y[ids].astype(np.float64)))]
+        probs = pyoracle.expf_array(((y[ids] - y[ids[0]]) / t).astype(np.float32)).astype(np.float64)
+        mass = math.fsum(probs)
+        j = int(np.searchsorted(np.cumsum(probs), float(w.uniforms[r]) * mass))
+        tok = int(ids[min(j, len(ids) - 1)])
+        assert boundary_shift(w, r, ref.token[r], ref.keep[r]) == (0.0, 0.0)
+        du, dp = boundary_shift(w, r, tok, len(ids))
+        if du > TOL_U:
+            over.append(r)
+    assert {8, 9, 10, 12, 13, 15} <= set(over), over
