@@ -14,7 +14,11 @@ event per step (a step then also holds the gap from one launch to the next),
 `roofline.achieved` from the same K launches each between two events (the
 kernel's own duration, `roofline.kernel_avg_us`).  The CPU baseline is the
 oracle restatement of the reference sampler, timed on this host's cores on the
-same workload.
+same workload; its results for input set 0 also check the GPU's tokens (after
+the timed region).  ``roofline.traffic`` comes from
+``profiles/traffic_<config>.json`` (rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
+tachyon_amd/traffic.py) only when that file was measured on the library
+loaded here (same SHA-256); otherwise it is null.
 
 Prints ONE JSON line.
 
@@ -45,9 +49,40 @@ DESCR = {
     "c5": "c5: B=1024 V=151936 nucleus p=.98 T=1.2 no top-k, R=1.05/256",
 }
 
+# kernels a step launches (batches of up to 16 rows take the split-row kernel
+# for their top-k rows)
+KERNELS = {
+    "c1": "split_kernel (one launch per tsm_sample step)",
+    "c2": "sample_kernel (one launch per tsm_sample step)",
+    "c3": "sample_kernel (one launch per tsm_sample step)",
+    "c4": "sample_kernel (one launch per tsm_sample step)",
+    "c5": "sample_kernel (one launch per tsm_sample step)",
+}
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def oracle_check(w, got_tokens, threads):
+    """Rows of input set 0 whose GPU token equals the oracle's."""
+    from oracle import pyoracle
+
+    ref = pyoracle.sample_batch(w, nthreads=threads)
+    same = int((ref.token == got_tokens).sum())
+    return {"rows": int(w.rows), "token_equal": same}
 
 
 def cpu_baseline(w, budget_s, threads):
@@ -74,7 +109,8 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(SEEDS))
     ap.add_argument("--sets", type=int, default=3, help="rotated input sets")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="no CPU baseline")
+    ap.add_argument("--no-check", action="store_true", help="no check of set 0's tokens against the oracle")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run N MiB device copies for counter calibration instead of the bench")
     args = ap.parse_args()
@@ -147,11 +183,31 @@ def main():
     alg_bytes = w0.algorithmic_bytes()
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
     rows_s = rows / (ms_step * 1e-3)
+
+    # outside the timed region: set 0's tokens against the oracle
+    check = None
+    if not args.no_check:
+        ctx.sample(batches[0], out)
+        torch.cuda.synchronize()
+        assert ctx.status() == 0
+        got = out.numpy()["token"]
+        log("[bench] checking set 0's tokens against the oracle")
+        check = oracle_check(w0, got, min(16, len(os.sched_getaffinity(0))))
+
+    from tachyon_amd import _lib
+    from tachyon_amd.traffic import library_sha256
+
     traffic = None
+    traffic_note = None
+    lib_sha = library_sha256(_lib.LIB_PATH)
     tfile = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(tfile):
         with open(tfile) as fh:
-            traffic = json.load(fh).get("hbm_bytes_per_step")
+            tj = json.load(fh)
+        if tj.get("library_sha256") == lib_sha:
+            traffic = tj.get("hbm_bytes_per_step")
+        else:
+            traffic_note = f"profiles/traffic_{args.config}.json was measured on another build of the library"
 
     cpu = None
     if not args.no_cpu:
@@ -161,6 +217,7 @@ def main():
         ncores = len(os.sched_getaffinity(0))
         v_all, steps_all, el_all = cpu_baseline(w0, args.cpu_seconds / 2, ncores)
         cpu = {"value": round(v, 1), "unit": "rows/s", "cores": ref_threads, "kind": "port",
+               "cpu_model": cpu_model(),
                "sample": f"{steps} full {args.config} batches ({steps * rows} rows) in {el:.1f}s with the "
                          f"reference's own row parallelism (min(ceil(B/4),4) threads)",
                "all_cores": {"value": round(v_all, 1), "cores": ncores, "sample": f"{steps_all * rows} rows"}}
@@ -183,9 +240,12 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_step": alg_bytes, "kernel_avg_us": round(kern_ms * 1e3, 2),
-                     "kernel": "sample_kernel (one launch per tsm_sample step)"},
+                     "kernel": KERNELS[args.config], "library_sha256": lib_sha[:16]},
         "cpu_baseline": cpu,
+        "oracle_check": check,
     }
+    if traffic_note:
+        rec["roofline"]["traffic_note"] = traffic_note
     ctx.close()
     print(json.dumps(rec), flush=True)
 

@@ -35,6 +35,7 @@
 // and slower.
 #include "tsm_sample.h"
 #include "tsm_nucleus.h"
+#include "tsm_serial.h"
 #include "tsm_split.h"
 
 namespace tsm {
@@ -79,6 +80,15 @@ __device__ __forceinline__ uint32_t* lds_hkey() { return reinterpret_cast<uint32
 __device__ __forceinline__ uint32_t* lds_hcnt() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashCnt); }
 __device__ __forceinline__ uint32_t* lds_shist() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSHist); }
 __device__ __forceinline__ uint32_t* lds_seg_pub() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg); }
+// One word per wave, written only by that wave: no other wave's write can
+// race its initialisation, so the stream needs no barrier for it.
+__device__ __forceinline__ uint32_t* lds_nan_wave() { return reinterpret_cast<uint32_t*>(lds_base() + kOffNanW); }
+// Some wave's word set: the row holds a NaN logit (a wave-wide read; after a
+// barrier that follows the stream).
+__device__ __forceinline__ bool row_has_nan() {
+    const uint32_t lane = lane_id();
+    return wave_ballot(lane < kBlock / kWave && lds_nan_wave()[lane] != 0u) != 0u;
+}
 __device__ __forceinline__ uint32_t* lds_seg_done() {
     return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg + (kBlock / kWave) * 4);
 }
@@ -729,6 +739,15 @@ __device__ __forceinline__ TileFlags tile_prep(const float (&v)[kVec][4], const 
         for (int e = 0; e < kVec * 4; e++)
             if (tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3) < n) valid |= 1u << e;
     }
+    // NaN logits: a logprobs row finds them in its logsumexp sum (tested
+    // after the stream); other rows compare, and a wave that meets one marks
+    // its own LDS word (no register carries it through the stream)
+    if (!logprobs) {
+        bool nan = false;
+#pragma unroll
+        for (int e = 0; e < kVec * 4; e++) nan |= ((valid >> e) & 1u) && v[e >> 2][e & 3] != v[e >> 2][e & 3];
+        if (wave_ballot(nan) && lane_id() == 0) lds_nan_wave()[tid / kWave] = 1u;
+    }
     // bitmap words first: their LDS latency overlaps the exponentials (words
     // past the row are read, in bounds, and masked off below)
     uint32_t bw[kVec];
@@ -824,6 +843,50 @@ __device__ __forceinline__ void stream_write(const float (&v)[kVec][4], const Ti
 
 // After the streaming pass: logsumexp and allowed count, then the pick (or
 // the distribution) and the logprobs of the row.
+__device__ __forceinline__ serial::Row serial_row(const Fin& f) {
+    serial::Row r;
+    r.x = f.rowp;
+    r.n = f.n;
+    r.hist = f.hist;
+    r.hlen = f.hist ? f.hlen : 0u;
+    r.mrow = f.mrow;
+    r.m = f.m;
+    r.P = f.P;
+    r.u = f.u;
+    return r;
+}
+
+// The serial path's LDS areas in the whole-row kernel: region A (the history
+// table and the finish's lists), which the stream no longer needs.
+__device__ __forceinline__ serial::Lds serial_lds(const Fin& f) {
+    serial::Lds s;
+    s.cnt = f.cnt();
+    s.val = f.ry();
+    s.id = f.rid();
+    s.comp = f.gcomp();
+    s.p = f.rp();
+    s.tile = kReTile;
+    return s;
+}
+
+// The raw top-n of a row holding a NaN (sampler.rs:305-311 through top_n):
+// ids in top_n's order, logprobs NaN (the row's logsumexp is NaN).  Wave 0.
+// Inlined, as finish_nan: the serial functions it calls take its local copies
+// (a reference into the kernel's argument block passed to a function that is
+// not inlined would turn the kernel's global loads into flat loads).
+__device__ __forceinline__ void nan_top_list(uint32_t* top_ids, float* top_lp, uint32_t top_stride, const Fin& f,
+                                             uint32_t nlp) {
+    const serial::Row r = serial_row(f);
+    const serial::Lds s = serial_lds(f);
+    const uint32_t k = serial::top_n_ref(r, s, nlp, false);
+    const uint32_t lane = lane_id();
+    if (lane < k) {
+        const size_t o = static_cast<size_t>(blockIdx.x) * top_stride + lane;
+        top_ids[o] = s.id[lane];
+        if (top_lp) top_lp[o] = __uint_as_float(0x7FC00000u);
+    }
+}
+
 __device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in, const Targets tg0,
                                            const uint32_t nlp, const float lref, const double lsum, uint32_t nallow,
                                            uint32_t bufn) {
@@ -1035,6 +1098,11 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in,
         if (a.out_prob) a.out_prob[row] = pk.prob;
         if (a.out_keep) a.out_keep[row] = pk.keep;
         if (m.logprobs && a.out_logprob) a.out_logprob[row] = f.rowp[pk.token] - lse;
+    }
+    if (row_has_nan()) {  // a nucleus row holding a NaN: its raw top-n in top_n's own order
+        TSM_LDS_SYNC();
+        if (tid < kWave && nlp > 0) nan_top_list(a.out_top_ids, a.out_top_lp, a.top_stride, f, nlp);
+        return;
     }
     if (tid < nraw) {
         const uint32_t id = static_cast<uint32_t>(raw_mine);
@@ -1669,6 +1737,78 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
     return true;
 }
 
+// Top_n-path rows (and sample()'s greedy shortcut) whose logits hold a NaN
+// (tsm_serial.h): wave 0 samples the row step by step.  The logprobs are
+// NaN, as the reference's logsumexp is then (sampler.rs:298-304).  A nucleus
+// row keeps the cutoff path, which a NaN never enters (it fails `l >=
+// cutoff`, sampler.rs:203); only its raw top-n is redone (nan_top_list).
+__device__ __forceinline__ void finish_nan(const SampleArgs& a, const Fin& f, uint32_t nlp) {
+    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+    const RowMode m = f.m;
+    const serial::Row r = serial_row(f);
+    const serial::Lds s = serial_lds(f);
+    constexpr float kNaN = __builtin_nanf("");
+    TSM_LDS_SYNC();
+    serial::Result res;
+    res.token = res.keep = res.len = 0;
+    res.prob = res.mass = 0.0f;
+    uint32_t* misc = lds_misc();
+    if (tid < kWave) {
+        res = serial::run(r, s, !a.distribution);
+        if (tid == 0) {
+            misc[M_TOKEN] = res.token;
+            misc[M_KEEP] = res.keep;
+            misc[M_PROB] = __float_as_uint(res.prob);
+            misc[M_MASS] = __float_as_uint(res.mass);
+        }
+    }
+    TSM_LDS_SYNC();
+    res.token = misc[M_TOKEN];
+    res.keep = misc[M_KEEP];
+    res.prob = __uint_as_float(misc[M_PROB]);
+    res.mass = __uint_as_float(misc[M_MASS]);
+    if (a.distribution) {
+        const uint32_t k = min(res.keep, a.dist_stride);
+        uint32_t* ids = a.dist_ids + static_cast<size_t>(row) * a.dist_stride;
+        float* probs = a.dist_probs + static_cast<size_t>(row) * a.dist_stride;
+        for (uint32_t j = tid; j < k; j += kBlock) {
+            ids[j] = s.id[j];
+            probs[j] = s.p[j] / res.mass;
+        }
+        if (res.keep > a.dist_stride && tid == 0) atomicOr(a.status, TSM_STATUS_DIST_TRUNCATED);
+        if (tid == 0) a.out_keep[row] = res.keep;
+        return;
+    }
+    if (tid == 0) {
+        a.out_token[row] = res.token;
+        if (a.out_prob) a.out_prob[row] = res.prob;
+        if (a.out_keep) a.out_keep[row] = res.keep;
+        if (m.logprobs && a.out_logprob) a.out_logprob[row] = kNaN;
+    }
+    if (nlp > 0) {
+        TSM_LDS_SYNC();  // the list areas are taken again
+        if (tid < kWave) nan_top_list(a.out_top_ids, a.out_top_lp, a.top_stride, f, nlp);
+    }
+}
+
+// finish_nan's arguments, handed over in LDS (the histogram area, unused
+// once the stream is done): the call then passes nothing in registers, so
+// the rare NaN branch adds no register pressure to the kernel's stream.
+struct NanCall {
+    SampleArgs a;
+    Fin f;
+    uint32_t nlp;
+};
+static_assert(sizeof(NanCall) <= kBins * 12, "NanCall fits the histogram area");
+__device__ __forceinline__ NanCall* nan_call() { return reinterpret_cast<NanCall*>(lds_base() + kOffHist); }
+
+__device__ __noinline__ void finish_nan_call() {
+    const SampleArgs a = nan_call()->a;
+    const Fin f = nan_call()->f;
+    const uint32_t nlp = nan_call()->nlp;
+    finish_nan(a, f, nlp);
+}
+
 template <bool kVecLoads>
 __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
@@ -1797,6 +1937,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     uint32_t seg0 = 0, seg_cap = 0, seg_fill = 0;
 
     // ---------------- streaming pass ----------------
+    if (lane == 0) lds_nan_wave()[wid] = 0u;
     LseAcc lse;
     mask_tail(v, 0, n);
     if (m.logprobs) {
@@ -2082,9 +2223,22 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         if (tid == 0 && (fill > kBufCap || misc[M_OVF] != 0u)) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
         bufn = min(fill, kBufCap);
     }
+    // a NaN logit (or +inf, whose steps make the sum NaN as well; the serial
+    // path is exact for those rows too) leaves a logprobs row's sum NaN
+    if (wave_ballot(m.logprobs && !(lse.sum == lse.sum)) && lane == 0) lds_nan_wave()[wid] = 1u;
     // the finish: one wave for the common rows, the whole block otherwise
     TSM_LDS_SYNC();
     const uint32_t flags = misc[M_FLAGS];
+    if (m.topk && row_has_nan()) {
+        if (tid == 0) {
+            nan_call()->a = a;
+            nan_call()->f = f;
+            nan_call()->nlp = nlp;
+        }
+        TSM_LDS_SYNC();
+        finish_nan_call();
+        return;
+    }
     if (tracking && !(flags & (ROWF_BUF_OVERFLOW | ROWF_SLOW_HISTORY)) && m.topk && !a.distribution &&
         m.want <= kWaveList && nlp <= kWaveList) {
         if (finish_wave(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn)) return;

@@ -44,7 +44,8 @@ constexpr uint32_t kOffTmp = kOffMiscD + 32 * 8;                 // u32[64] scan
 constexpr uint32_t kSBins = 512;                                 // stream histogram bins per threshold
 constexpr uint32_t kOffSHist = kOffTmp + 64 * 4;                 // 2 x u32[kSBins]
 constexpr uint32_t kOffSeg = kOffSHist + 2 * kSBins * 4;         // per wave: published fill, counted fill
-constexpr uint32_t kSmem = kOffSeg + 2 * (kBlock / kWave) * 4;
+constexpr uint32_t kOffNanW = kOffSeg + 2 * (kBlock / kWave) * 4;  // per wave: met a NaN logit
+constexpr uint32_t kSmem = kOffNanW + (kBlock / kWave) * 4;
 static_assert(kOffGather % 8 == 0 && (kOffHist + kBins * 4) % 8 == 0 && kOffBuf % 8 == 0 && kOffPen % 8 == 0 &&
                   kOffMiscD % 8 == 0,
               "u64 / f64 LDS records are 8-byte aligned");

@@ -34,6 +34,7 @@
 // Segments that hold too many candidates for their area (ties) redo their
 // thresholds exactly by radix selection over the segment (re-read from L2).
 #include "tsm_split.h"
+#include "tsm_serial.h"
 
 namespace tsm {
 namespace split {
@@ -925,7 +926,7 @@ __device__ __forceinline__ void fin_row(const SplitArgs& a, const FinSrc& S, con
     }
 
     // ---- outputs ----
-    const bool bad = token >= n || (flags_row & SEG_NAN);
+    const bool bad = token >= n;
     if (bad && tid == 0) atomicOr(a.s.status, TSM_STATUS_INTERNAL);
     if (token >= n) token = 0;
     if (a.s.distribution) {
@@ -1023,6 +1024,74 @@ __device__ __forceinline__ float group_threshold(const float (&gm)[8], uint32_t 
 }
 
 // ---- the kernel ----------------------------------------------------------------------
+
+// A row whose logits hold a NaN (tsm_serial.h): wave 0 of the row's last
+// workgroup samples it step by step from the row in memory; the LDS of the
+// history table and of the finish's lists holds the serial path's areas.
+// The logprobs are NaN, as the reference's logsumexp is (sampler.rs:298-304).
+__device__ __noinline__ void fin_nan(const SplitArgs& a, const serial::Row& r, uint32_t row, uint32_t nlp) {
+    const uint32_t tid = threadIdx.x;
+    constexpr float kNaN = __builtin_nanf("");
+    serial::Lds s;
+    s.tile = 4096;
+    s.cnt = s_hkey();                                                       // 8 KB
+    s.val = reinterpret_cast<float*>(lds_base() + kOffHKey + 8192);         // 4 KB
+    s.id = reinterpret_cast<uint32_t*>(lds_base() + kOffHKey + 12288);      // 4 KB
+    s.comp = s_lq();
+    s.p = s_lp();
+    static_assert(kHSlots * 8 >= 16384 && kListMax >= kMaxWindow, "serial areas");
+    TSM_LDS_SYNC();
+    serial::Result res;
+    res.token = res.keep = res.len = 0;
+    res.prob = res.mass = 0.0f;
+    if (tid < kWave) {
+        res = serial::run(r, s, !a.s.distribution);
+        if (tid == 0) {
+            s_misc()[MS_PICK] = res.token;
+            s_misc()[MS_PICK + 1] = res.keep;
+            s_misc()[MS_PICK + 2] = __float_as_uint(res.prob);
+            s_misc()[MS_PICK + 3] = __float_as_uint(res.mass);
+        }
+    }
+    TSM_LDS_SYNC();
+    res.token = s_misc()[MS_PICK];
+    res.keep = s_misc()[MS_PICK + 1];
+    res.prob = __uint_as_float(s_misc()[MS_PICK + 2]);
+    res.mass = __uint_as_float(s_misc()[MS_PICK + 3]);
+    if (a.s.distribution) {
+        const uint32_t k = min(res.keep, a.s.dist_stride);
+        uint32_t* ids = a.s.dist_ids + static_cast<size_t>(row) * a.s.dist_stride;
+        float* probs = a.s.dist_probs + static_cast<size_t>(row) * a.s.dist_stride;
+        for (uint32_t j = tid; j < k; j += kSB) {
+            ids[j] = s.id[j];
+            probs[j] = s.p[j] / res.mass;
+        }
+        if (res.keep > a.s.dist_stride && tid == 0) atomicOr(a.s.status, TSM_STATUS_DIST_TRUNCATED);
+        if (tid == 0) a.s.out_keep[row] = res.keep;
+    } else {
+        if (tid == 0) {
+            a.s.out_token[row] = res.token;
+            if (a.s.out_prob) a.s.out_prob[row] = res.prob;
+            if (a.s.out_keep) a.s.out_keep[row] = res.keep;
+            if (r.m.logprobs && a.s.out_logprob) a.s.out_logprob[row] = kNaN;
+        }
+        if (nlp > 0) {
+            TSM_LDS_SYNC();  // the list areas are taken again
+            if (tid < kWave) {
+                const uint32_t k = serial::top_n_ref(r, s, nlp, false);
+                if (tid < k) {
+                    const size_t o = static_cast<size_t>(row) * a.s.top_stride + tid;
+                    a.s.out_top_ids[o] = s.id[tid];
+                    if (a.s.out_top_lp) a.s.out_top_lp[o] = kNaN;
+                }
+            }
+        }
+    }
+    if (r.m.logprobs && a.s.out_top_ids && r.m.nlp > a.s.top_stride && tid == 0)
+        atomicOr(a.s.status, TSM_STATUS_BAD_PARAMS);
+    // counters back to 0 for the next call (every segment has arrived)
+    if (tid == 0) dev_st64(&a.w.row_ctr[row], 0ull);
+}
 
 template <bool kVecLoads>
 __global__ __launch_bounds__(kSB) void split_kernel(SplitArgs a) {
@@ -1599,6 +1668,19 @@ __global__ __launch_bounds__(kSB) void split_kernel(SplitArgs a) {
         ls = block_sum_d(ls);
         lse = xmax_row + static_cast<float>(log(ls));
         if (flags_row & SEG_NAN) lse = kNaNf;  // a NaN logit makes the reference's sum NaN
+    }
+    if (flags_row & SEG_NAN) {
+        serial::Row r;
+        r.x = rowp;
+        r.n = n;
+        r.hist = (a.s.hist_ids && hlen) ? a.s.hist_ids + h0 : nullptr;
+        r.hlen = r.hist ? hlen : 0u;
+        r.mrow = mrow;
+        r.m = m;
+        r.P = P;
+        r.u = a.s.distribution ? 0.0f : a.s.uniforms[row];
+        fin_nan(a, r, row, nlp);
+        return;
     }
     FinSrc S;
     S.cbase = rcand;

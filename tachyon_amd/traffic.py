@@ -14,16 +14,31 @@ Usage (paths are the ``*_counter_collection.csv`` files rocprofv3 wrote):
         --algorithmic-bytes 161506304 --out traffic_c4.json
 
 It prints a short text summary and writes the JSON that ``bench.py`` reads
-for ``roofline.traffic``.
+for ``roofline.traffic``.  The JSON carries the SHA-256 of the sampling
+library the counters were taken on (``--library``, by default the in-tree
+build); ``bench.py`` reports the traffic only when the library it loaded has
+the same hash.
 """
 from __future__ import annotations
 
 import argparse
 import csv
+import hashlib
 import json
+import os
 import statistics
 
 KERNEL = "sample_kernel"
+DEFAULT_LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libtachyon_sampler.so")
+
+
+def library_sha256(path: str) -> str:
+    """SHA-256 (hex) of a built library file."""
+    h = hashlib.sha256()
+    with open(path, "rb") as fh:
+        for chunk in iter(lambda: fh.read(1 << 20), b""):
+            h.update(chunk)
+    return h.hexdigest()
 
 
 def per_dispatch(path: str, counter: str, name_part: str) -> list[float]:
@@ -65,6 +80,7 @@ def main() -> None:
     ap.add_argument("--copy-mb", type=int, required=True)
     ap.add_argument("--algorithmic-bytes", type=int, required=True)
     ap.add_argument("--out", required=True)
+    ap.add_argument("--library", default=DEFAULT_LIBRARY, help="the library the counter runs loaded")
     args = ap.parse_args()
 
     copy_bytes = args.copy_mb << 20
@@ -81,6 +97,7 @@ def main() -> None:
     write_b = statistics.mean(kw) * 1024.0 * f_write
     total = fetch_b + write_b
     rec = {
+        "library_sha256": library_sha256(args.library),
         "hbm_bytes_per_step": int(round(total)),
         "fetch_bytes_per_step": int(round(fetch_b)),
         "write_bytes_per_step": int(round(write_b)),

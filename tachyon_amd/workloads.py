@@ -229,11 +229,12 @@ CONFIGS = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5}
 
 
 def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, mask_frac=0.3,
-                logprobs=True, hist_len=16, penalties=True, mode="mixed", sigma=2.0, outlier=None):
+                logprobs=True, hist_len=16, penalties=True, mode="mixed", sigma=2.0, outlier=None,
+                specials=False):
     """Small random workload for parity tests: mixed per-row settings, optional
     heavy ties (integer-valued logits), masks and histories.  `outlier` sets
     id 0 of every row to that value (a narrow cluster of logits next to one
-    far value)."""
+    far value); `specials` puts NaN, +inf and -inf logits into the rows."""
     rng = np.random.default_rng(seed)
     stride = stride or vocab
     if ties:
@@ -243,6 +244,25 @@ def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, 
         x = (rng.standard_normal((rows, stride)) * sigma).astype(np.float32)
     if outlier is not None:
         x[:, 0] = np.float32(outlier)
+    if specials:
+        # row r by r % 6: NaNs at 3 random ids, two +inf, 70% -inf, all -inf,
+        # a NaN at id 0, one +inf and two NaNs
+        srng = np.random.default_rng(seed + 7777)
+        for r in range(rows):
+            k = r % 6
+            if k == 0:
+                x[r, srng.integers(0, vocab, 3)] = np.nan
+            elif k == 1:
+                x[r, srng.integers(0, vocab, 2)] = np.inf
+            elif k == 2:
+                x[r, :vocab][srng.random(vocab) < 0.7] = -np.inf
+            elif k == 3:
+                x[r, :vocab] = -np.inf
+            elif k == 4:
+                x[r, 0] = np.nan
+            else:
+                x[r, srng.integers(0, vocab, 1)] = np.inf
+                x[r, srng.integers(0, vocab, 2)] = np.nan
     p = make_params(rows)
     for r in range(rows):
         kind = mode if mode != "mixed" else ["greedy", "topk", "topp", "nucleus", "minp", "all"][r % 6]

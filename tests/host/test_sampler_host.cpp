@@ -266,7 +266,7 @@ void penalty_can_flip_the_choice(BatchSampler& bs) {
 // Several sequences over many steps, batched: every step's tokens and every
 // sequence's RNG state equal the oracle's per-sequence Sampler.
 void sequences_match_the_oracle(BatchSampler& bs) {
-    const uint32_t rows = 12, vocab = 3000;
+    const uint32_t rows = 13, vocab = 3000;
     std::mt19937 g(11);
     std::vector<SamplerConfig> cs;
     for (uint32_t r = 0; r < rows; r++) {
@@ -275,6 +275,7 @@ void sequences_match_the_oracle(BatchSampler& bs) {
         if (r % 6 == 1) c.temperature = 0.0f;                     // greedy with penalty: one draw
         if (r % 6 == 2) c.top_k = 500, c.top_p = 0.98f;           // a wide window
         if (r % 6 == 3) c.min_p = 0.05f, c.presence_penalty = 0.3f;
+        if (r == 12) c = SamplerConfig::greedy();                 // constrained below: sample_with() draws
         cs.push_back(c);
     }
     std::vector<Sampler> ss;
@@ -296,7 +297,7 @@ void sequences_match_the_oracle(BatchSampler& bs) {
             req[r].sampler = &ss[r];
             req[r].recent = recent[r].data();
             req[r].n_recent = recent[r].size();
-            req[r].constrained = (r % 4 == 3);
+            req[r].constrained = (r % 4 == 3) || r == 12;
             if (req[r].constrained) {
                 // a third of the rows' masks allow nothing at some steps: no draw
                 const bool none = (r % 3 == 0) && (step % 5 == 4);

@@ -23,7 +23,20 @@ REL, ABS = 1e-5, 1e-6
 
 
 def close(a, b, rel=REL, abs_=ABS):
-    return abs(float(a) - float(b)) <= abs_ + rel * abs(float(b))
+    """Within the logprob tolerance; NaN matches NaN only (a row holding a
+    NaN logit has a NaN logsumexp)."""
+    a, b = float(a), float(b)
+    if b != b or a != a:
+        return a != a and b != b
+    return abs(a - b) <= abs_ + rel * abs(b)
+
+
+def same_f32(a, b):
+    """Bit-exact, except that any NaN matches any NaN (the payload of a NaN
+    result is not the reference's arithmetic)."""
+    if a != a or b != b:
+        return a != a and b != b
+    return np.float32(a).tobytes() == np.float32(b).tobytes()
 
 
 def boundary_shift(w, r, token, keep):
@@ -47,7 +60,7 @@ def check(w, got, ref, label):
         same_token = got["token"][r] == ref.token[r]
         if same_token and got["keep"][r] == ref.keep[r]:
             exact_rows += 1
-            assert got["prob"][r].tobytes() == ref.prob[r].tobytes(), tag + f" prob {got['prob'][r]} {ref.prob[r]}"
+            assert same_f32(got["prob"][r], ref.prob[r]), tag + f" prob {got['prob'][r]} {ref.prob[r]}"
         else:
             shift = boundary_shift(w, r, got["token"][r], got["keep"][r])
             assert shift is not None and shift[0] <= TOL_U and shift[1] <= TOL_P, (
@@ -104,7 +117,21 @@ RANDOM_CASES = [
     dict(seed=16, vocab=15000, rows=6, mode="nucleus", ties=True),
     dict(seed=17, vocab=15000, rows=6, mode="nucleus", sigma=0.01, outlier=-1.0e4),
     dict(seed=18, vocab=60000, rows=12, mode="nucleus", sigma=0.003, outlier=-50.0, masked=True, mask_frac=0.5),
+    # NaN, +inf and -inf logits (a NaN at id 0, NaNs at random ids, +inf
+    # spikes, rows 70% -inf, rows all -inf), on the split-row kernel (12 rows)
+    # and the whole-row kernel (20 rows)
+    dict(seed=19, vocab=300, rows=12, specials=True),
+    dict(seed=20, vocab=3000, rows=20, specials=True, masked=True),
+    dict(seed=24, vocab=3000, rows=12, specials=True, mode="topk", masked=True, mask_frac=0.02),
+    dict(seed=25, vocab=5000, rows=20, specials=True, mode="nucleus"),
+    # histories longer than the LDS history table (2048 ids): penalties
+    # applied on re-reads
+    dict(seed=26, vocab=3000, rows=20, hist_len=4000),
+    # penalties over a vocabulary beyond the history bitmap (262144 ids)
+    dict(seed=27, vocab=300000, rows=20, hist_len=64),
 ]
 
 DIST_CASES = [(21, dict(vocab=500, mode="mixed")), (22, dict(vocab=3000, mode="minp")),
-              (23, dict(vocab=3000, mode="topk", ties=True))]
+              (23, dict(vocab=3000, mode="topk", ties=True)),
+              # kept sets beyond the 1024 written entries (DIST_TRUNCATED)
+              (28, dict(vocab=6000, mode="nucleus", sigma=0.5))]

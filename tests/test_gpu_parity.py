@@ -36,6 +36,9 @@ def say(msg):
     sys.stdout.flush()
 
 
+CTX_VOCAB = 152064
+
+
 @pytest.fixture(scope="module")
 def ctx():
     import torch
@@ -43,7 +46,7 @@ def ctx():
     assert torch.cuda.is_available(), "no GPU"
     from tachyon_amd.device import SamplerContext
 
-    c = SamplerContext(max_rows=1024, max_vocab=152064)
+    c = SamplerContext(max_rows=1024, max_vocab=CTX_VOCAB)
     yield c
     c.close()
 
@@ -93,8 +96,17 @@ def test_device_expf_matches_glibc(ctx):
 
 @pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"rand{c['seed']}" for c in RANDOM_CASES])
 def test_parity_random(ctx, case):
+    from tachyon_amd.device import SamplerContext
+
     w = wl.random_case(**case)
-    run_case(ctx, w, f"rand{case['seed']}")
+    if w.usable <= CTX_VOCAB:
+        run_case(ctx, w, f"rand{case['seed']}")
+        return
+    big = SamplerContext(max_rows=w.rows, max_vocab=w.usable)  # vocabularies past the shared context's
+    try:
+        run_case(big, w, f"rand{case['seed']}")
+    finally:
+        big.close()
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
@@ -184,6 +196,7 @@ def test_distribution_parity(ctx):
     from oracle import pyoracle
     from tachyon_amd.device import upload
 
+    ctx.status()  # clears what earlier calls left
     for seed, kw in DIST_CASES:
         w = wl.random_case(seed=seed, rows=12, **kw)
         say(f"[gpu] distribution seed {seed}")
@@ -193,6 +206,9 @@ def test_distribution_parity(ctx):
         ids, ps, keep = ids.cpu().numpy().view(np.uint32), ps.cpu().numpy(), keep.cpu().numpy().view(np.uint32)
         rids, rps, rkeep = pyoracle.distribution_batch(w, 1024)
         check_distribution(w, ids, ps, keep, rids, rps, rkeep, f"dist{seed}")
+        # a kept set beyond the written entries is reported
+        st = ctx.status()
+        assert bool(st & 4) == bool((rkeep > 1024).any()), (seed, st)
 
 
 def test_abi_rejects_bad_arguments(ctx):

@@ -414,3 +414,50 @@ def test_boundary_check_rejects_exact_arithmetic_picks(oracle):
         if du > TOL_U:
             over.append(r)
     assert {8, 9, 10, 12, 13, 15} <= set(over), over
+
+
+def test_nan_and_inf_semantics_hand_derived(oracle):
+    """NaN and infinite logits, traced by hand through sampler.rs: top_n's
+    insertion with partition_point (the halving search: mid = lo + (hi - lo)
+    / 2, lo = mid + 1 while w >= v holds), `v > floor` false for NaN, argmax's
+    strict '>', NaN probabilities that no fold step decides, and pick
+    falling through to idx[keep - 1] (sampler.rs:139-150, :267-285, :314-322)."""
+    nan, inf = np.nan, np.inf
+    # argmax: nothing beats a NaN at 0; elsewhere a NaN never wins
+    assert oracle.argmax([1.0, nan, 3.0]) == 2
+    assert oracle.argmax([nan, 5.0, 7.0]) == 0
+    assert oracle.argmax([2.0, nan, 2.0]) == 0
+    # [NaN, 1, 2], n=2: NaN enters first; 1 goes before it (NaN >= 1 is
+    # false); the list is full with floor NaN, so 2 is never inserted
+    v, i = oracle.top_n([nan, 1.0, 2.0], 2)
+    assert i.tolist() == [1, 0] and v[0] == 1.0 and np.isnan(v[1])
+    # [3, NaN, 1, 5], n=3: [3] -> [NaN, 3] -> [NaN, 3, 1] (probe at 3: 3 >= 1)
+    # -> 5 > floor 1: probes 3 >= 5 no, NaN >= 5 no -> [5, NaN, 3]
+    v, i = oracle.top_n([3.0, nan, 1.0, 5.0], 3)
+    assert i.tolist() == [3, 1, 0] and v[0] == 5.0 and np.isnan(v[1]) and v[2] == 3.0
+    # [0, inf, 1, inf], n=3: ties of inf keep the lower id first
+    v, i = oracle.top_n([0.0, inf, 1.0, inf], 3)
+    assert i.tolist() == [1, 3, 2]
+
+    def one(x, **kw):
+        x = np.asarray([x], np.float32)
+        w = wl.Workload("nan", x, x.shape[1], wl.make_params(1, **kw), None, None, None,
+                        np.array([0.25], np.float32))
+        return oracle.sample_batch(w)
+
+    # ranked [(1, id 1), (NaN, id 0)]: p = [1, NaN], total NaN: acc never
+    # reaches top_p, keep = 2, r = u * NaN never <= 0: the last kept, id 0
+    r = one([nan, 1.0, 2.0, 0.5], temperature=1.0, top_k=2, top_p=0.9)
+    assert r.token[0] == 0 and r.keep[0] == 2 and np.isnan(r.prob[0])
+    # best +inf: p_0 = exp((inf - inf) / t) = NaN, so again the last kept (id 2)
+    r = one([0.0, inf, 1.0, inf], temperature=1.0, top_k=3, top_p=0.5)
+    assert r.token[0] == 2 and r.keep[0] == 3
+    # every logit -inf: top_n keeps id order, p = exp(NaN) = NaN: the last, id 3;
+    # sample()'s greedy shortcut is argmax: id 0
+    r = one([-inf] * 4, temperature=1.0)
+    assert r.token[0] == 3 and r.keep[0] == 4
+    r = one([-inf] * 4, temperature=0.0)
+    assert r.token[0] == 0
+    # a NaN at id 0 and greedy: argmax returns 0 whatever follows
+    r = one([nan, 9.0, 1.0], temperature=0.0)
+    assert r.token[0] == 0
