@@ -22,7 +22,10 @@
  * src/gpu/mod.rs:467-480): a NULL handle or a nonzero int status, and a
  * NUL-terminated message written into the caller's (err, errlen) buffer.
  * "Nothing allowed" is not an error: such a row returns the argmax of its raw
- * logits, as the reference does (src/sampler.rs:139-141).
+ * logits, as the reference does (src/sampler.rs:139-141).  Neither are NaN or
+ * infinite logits: such rows get the reference's result (top_n's insertion
+ * order, src/sampler.rs:267-285; argmax's first index, :314-322), with NaN
+ * probabilities and logprobs where the reference's are NaN.
  */
 #ifndef TACHYON_SAMPLER_H
 #define TACHYON_SAMPLER_H
@@ -173,8 +176,10 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
 #define TSM_STATUS_HISTORY_TOO_LONG 1u
 #define TSM_STATUS_BAD_PARAMS       2u
 #define TSM_STATUS_DIST_TRUNCATED   4u
-#define TSM_STATUS_INTERNAL         8u /* a selection found no element (e.g. a
-                                          row of NaN logits); token 0 written */
+#define TSM_STATUS_INTERNAL         8u /* a selection found no element (not
+                                          expected: rows holding NaN or
+                                          infinite logits are sampled as the
+                                          reference does); token 0 written */
 #define TSM_STATUS_ROW_KIND        16u /* a row of a kind the batch's row_kinds
                                           left out: token 0 written           */
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);
