@@ -111,6 +111,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="no CPU baseline")
     ap.add_argument("--no-check", action="store_true", help="no check of set 0's tokens against the oracle")
+    ap.add_argument("--json-mask", action="store_true",
+                    help="time the mask producer (tsm_json_mask) instead: 256 JsonObject rows over a "
+                         "151936-token synthetic vocabulary")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run N MiB device copies for counter calibration instead of the bench")
     args = ap.parse_args()
@@ -130,6 +133,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"[bench] copied {args.calib_copy_mb} MiB x5")
+        return
+
+    if args.json_mask:
+        bench_json_mask(args)
         return
 
     from tachyon_amd import workloads as wl
@@ -247,6 +254,67 @@ def main():
     if traffic_note:
         rec["roofline"]["traffic_note"] = traffic_note
     ctx.close()
+    print(json.dumps(rec), flush=True)
+
+
+def bench_json_mask(args):
+    """One step of the mask producer: 256 rows in states from random JSON
+    prefixes, every token of a 151936-token synthetic vocabulary; checked
+    against the oracle's JsonObject on 8 rows after the timed region."""
+    import torch
+
+    from tachyon_amd import workloads as wl
+    from tachyon_amd.constrain import DeviceVocab, HostVocab, JsonConstraint, json_mask, pack_states
+
+    rows, V = 256, wl.QWEN_VOCAB
+    toks, special = wl.json_vocab(V, seed=0x15A0)
+    hv = HostVocab.from_tokens(toks, special)
+    dv = DeviceVocab(hv)
+    prefixes = wl.json_prefixes(rows, seed=0x15A4)
+    cs = []
+    for p in prefixes:
+        c = JsonConstraint()
+        c.advance(p)
+        cs.append(c)
+    st = torch.from_numpy(pack_states(cs)).cuda()
+    stride = (V + 31) // 32
+    mask = torch.zeros(rows, stride, dtype=torch.int32, device="cuda")
+    for _ in range(args.warmup):
+        json_mask(dv, st, rows, V, mask, stride)
+    torch.cuda.synchronize()
+    ea = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    eb = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        ea[i].record()
+        json_mask(dv, st, rows, V, mask, stride)
+        eb[i].record()
+    torch.cuda.synchronize()
+    us = sum(ea[i].elapsed_time(eb[i]) for i in range(args.steps)) / args.steps * 1e3
+    check = None
+    if not args.no_check:
+        from oracle import pyoracle
+
+        import numpy as np
+
+        got = mask.cpu().numpy().view(np.uint32)
+        same = 0
+        for r in range(0, rows, rows // 8):
+            o = pyoracle.JsonOracle()
+            o.advance(prefixes[r])
+            same += int((got[r] == o.mask(hv, V)).all())
+        check = {"rows": 8, "mask_equal": same}
+    alg = int(hv.offsets.nbytes + hv.bytes.nbytes + hv.special.nbytes + rows * stride * 4)
+    rec = {"metric": "JsonObject allow-masks per second (rows x 151936 tokens)", "value": round(rows / (us * 1e-6), 1),
+           "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "u8", "data": "synthetic",
+           "config": {"workload": "tsm_json_mask: 256 rows, states from random JSON prefixes, synthetic vocab",
+                      "rows": rows, "vocab": V},
+           "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                        "algorithmic_bytes_per_step": alg, "kernel_avg_us": round(us, 2),
+                        "kernel": "json_mask_kernel (one launch per step)"},
+           "cpu_baseline": None, "oracle_check": check}
     print(json.dumps(rec), flush=True)
 
 

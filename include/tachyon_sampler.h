@@ -205,6 +205,68 @@ int tsm_sample_static(void* stream, const tsm_batch* batch, const tsm_outputs* o
  * `has_mask` whether the batch passes a mask. */
 uint32_t tsm_row_kind(const tsm_row_params* p, uint32_t usable, uint32_t hist_len, int has_mask);
 
+/*
+ * ---- The mask producer: a JSON-object constraint -> packed allow-bits -------
+ *
+ * Tachyon checks `c.allows(tok, id)` (src/constrain.rs:286-290) for each id the
+ * sampler probes (src/scheduler.rs:653-656).  These entry points produce a
+ * whole row of those answers at once on the GPU, in the mask layout
+ * tsm_batch.mask consumes, for rows whose constraint is a JsonObject
+ * (OutputFormat::JsonObject, src/constrain.rs:14-33: `response_format:
+ * json_object`).  The automaton's state lives with the host-side sequence, as
+ * the reference's Box<dyn Constraint> does; each step the host passes every
+ * constrained row's state (12 bytes) and gets its mask row.
+ */
+
+/* JsonObject's state (src/constrain.rs:88-93): the automaton state, the
+ * stack of open containers (bit i of `stack`: level i is an object; at most
+ * 32 levels) and the whitespace run.  Built by tsm_json_init and advanced by
+ * tsm_json_advance only; the fields are not an interface. */
+typedef struct tsm_json_state {
+    uint32_t stack;
+    uint8_t  depth;
+    uint8_t  state;
+    uint8_t  aux;
+    uint8_t  len;
+    uint8_t  whitespace;
+    uint8_t  pad[3];
+} tsm_json_state;
+
+/* The tokenizer's token bytes (src/tokenizer.rs:189-195), in device memory:
+ * token t's bytes are bytes[offsets[t] .. offsets[t+1]).  Ids at or above
+ * n_tokens have no bytes (never allowed).  `special` (may be NULL) holds one
+ * bit per token, LSB-first: set = a special token, never allowed. */
+typedef struct tsm_vocab {
+    const uint8_t*  bytes;
+    const uint32_t* offsets;   /* [n_tokens + 1] */
+    const uint32_t* special;   /* [ceil(n_tokens / 32)] or NULL */
+    uint32_t        n_tokens;
+    uint32_t        reserved;  /* must be 0 */
+} tsm_vocab;
+
+/* JsonObject::default() (src/constrain.rs:95-103).  Host function. */
+void tsm_json_init(tsm_json_state* s);
+/* Constraint::advance with the chosen token's bytes (src/constrain.rs:292-296,
+ * called at src/scheduler.rs:698).  Host function. */
+void tsm_json_advance(tsm_json_state* s, const uint8_t* bytes, size_t n);
+/* JsonObject::accepts_bytes (src/constrain.rs:280-283): 1 if every byte steps
+ * a copy of the automaton.  Host function. */
+int tsm_json_accepts(const tsm_json_state* s, const uint8_t* bytes, size_t n);
+/* Constraint::is_complete (src/constrain.rs:298-300).  Host function. */
+int tsm_json_is_complete(const tsm_json_state* s);
+
+/*
+ * Writes the allow-bits of `rows` rows: bit b of word w of row r (mask +
+ * r*mask_stride) is set exactly when JsonObject::allows holds for token 32w+b
+ * in state states[r] (not special, has bytes, and accepts_bytes); ids at or
+ * above `usable` get 0 bits.  `states` and `mask` are device pointers;
+ * mask_stride >= ceil(usable / 32).  Queued on `stream`; allocates nothing.
+ * Replaces: the `&|t| c.allows(tok, t)` closure of src/scheduler.rs:653-656
+ * for JsonObject constraints, evaluated for the whole vocabulary.
+ */
+int tsm_json_mask(void* stream, const tsm_vocab* vocab, const tsm_json_state* states, uint32_t rows,
+                  uint32_t usable, uint32_t* mask, uint32_t mask_stride, char* err, size_t errlen);
+
 /* Library version string, e.g. "tachyon-sampler 0.1 gfx950". */
 const char* tsm_version(void);
 

@@ -121,6 +121,23 @@ def lib():
         L.or_reconcile.argtypes = [vp, ctypes.c_uint32, vp, vp, ctypes.c_size_t, vp, ctypes.c_float,
                                    ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                    ctypes.POINTER(ctypes.c_double)]
+        L.or_json_new.restype = vp
+        L.or_json_new.argtypes = []
+        L.or_json_free.restype = None
+        L.or_json_free.argtypes = [vp]
+        L.or_json_clone.restype = vp
+        L.or_json_clone.argtypes = [vp]
+        L.or_json_advance.restype = None
+        L.or_json_advance.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
+        L.or_json_accepts.restype = ctypes.c_int
+        L.or_json_accepts.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
+        L.or_json_is_complete.restype = ctypes.c_int
+        L.or_json_is_complete.argtypes = [vp]
+        L.or_json_check.restype = None
+        L.or_json_check.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int),
+                                    ctypes.POINTER(ctypes.c_int)]
+        L.or_json_mask.restype = None
+        L.or_json_mask.argtypes = [vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp]
         _lib = L
     return _lib
 
@@ -312,3 +329,44 @@ def reconcile(w, r, token, keep):
     rc = lib().or_reconcile(_vp(x), w.usable, _vp(prm), _vp(rec) if nrec else None, nrec, _vp(m),
                             float(w.uniforms[r]), int(token), int(keep), ctypes.byref(du), ctypes.byref(dp))
     return None if rc else (du.value, dp.value)
+
+
+# ---- JsonObject (constrain.rs), json_oracle.cpp -------------------------------
+
+class JsonOracle:
+    """The reference's JsonObject constraint (constrain.rs:88-302)."""
+
+    def __init__(self, _h=None):
+        self._h = _h if _h is not None else lib().or_json_new()
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and _lib is not None:
+            _lib.or_json_free(self._h)
+            self._h = None
+
+    def clone(self):
+        return JsonOracle(lib().or_json_clone(self._h))
+
+    def advance(self, b: bytes):
+        lib().or_json_advance(self._h, b, len(b))
+
+    def accepts(self, b: bytes) -> bool:
+        return bool(lib().or_json_accepts(self._h, b, len(b)))
+
+    def is_complete(self) -> bool:
+        return bool(lib().or_json_is_complete(self._h))
+
+    def mask(self, vocab, usable):
+        """allows() for ids [0, usable) as packed u32 words."""
+        words = np.zeros((usable + 31) // 32, np.uint32)
+        lib().or_json_mask(self._h, _vp(vocab.bytes), _vp(vocab.offsets),
+                           None if vocab.special is None else _vp(vocab.special),
+                           vocab.n_tokens, usable, _vp(words))
+        return words
+
+
+def json_check(text: bytes):
+    """constrain.rs tests' check(): (accepts_bytes, is_complete after advance)."""
+    ok, done = ctypes.c_int(), ctypes.c_int()
+    lib().or_json_check(text, len(text), ctypes.byref(ok), ctypes.byref(done))
+    return bool(ok.value), bool(done.value)

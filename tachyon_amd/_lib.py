@@ -46,8 +46,31 @@ class TsmOutputs(ctypes.Structure):
     ]
 
 
+class TsmJsonState(ctypes.Structure):
+    _fields_ = [
+        ("stack", u32),
+        ("depth", ctypes.c_uint8),
+        ("state", ctypes.c_uint8),
+        ("aux", ctypes.c_uint8),
+        ("len", ctypes.c_uint8),
+        ("whitespace", ctypes.c_uint8),
+        ("pad", ctypes.c_uint8 * 3),
+    ]
+
+
+class TsmVocab(ctypes.Structure):
+    _fields_ = [
+        ("bytes", vp),
+        ("offsets", vp),
+        ("special", vp),
+        ("n_tokens", u32),
+        ("reserved", u32),
+    ]
+
+
 SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version",
-           "tsm_row_kind", "tsm_sample_static"]
+           "tsm_row_kind", "tsm_sample_static", "tsm_json_init", "tsm_json_advance", "tsm_json_accepts",
+           "tsm_json_is_complete", "tsm_json_mask"]
 ROWKIND_SPLIT = 1
 ROWKIND_WHOLE = 2
 
@@ -85,6 +108,18 @@ def lib():
                                         ctypes.c_char_p, ctypes.c_size_t]
         L.tsm_row_kind.restype = u32
         L.tsm_row_kind.argtypes = [vp, u32, u32, ctypes.c_int]
+        js = ctypes.POINTER(TsmJsonState)
+        L.tsm_json_init.restype = None
+        L.tsm_json_init.argtypes = [js]
+        L.tsm_json_advance.restype = None
+        L.tsm_json_advance.argtypes = [js, ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_json_accepts.restype = ctypes.c_int
+        L.tsm_json_accepts.argtypes = [js, ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_json_is_complete.restype = ctypes.c_int
+        L.tsm_json_is_complete.argtypes = [js]
+        L.tsm_json_mask.restype = ctypes.c_int
+        L.tsm_json_mask.argtypes = [vp, ctypes.POINTER(TsmVocab), vp, u32, u32, vp, u32, ctypes.c_char_p,
+                                    ctypes.c_size_t]
         _lib = L
     return _lib
 

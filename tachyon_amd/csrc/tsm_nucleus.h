@@ -933,9 +933,11 @@ __device__ void plan_a(float T, float top_p) {
         const double a = s / T, a_end = s_end / T;
         const double lo = a * (1.0 - kPlanEps), hi = a * (1.0 + kPlanEps);
         plan_range(lo, hi, false, 16u, PF_TWO_A, PF_MUST_A, &pw);
-        const bool decides = a <= top_p * (1.0 + kPredEps) && a_end * (1.0 + kPredEps) >= top_p;
-        if ((pw & PF_MUST_A) || decides ||
-            binade_of(static_cast<float>(a_end * (1.0 + kPredEps))) != binade_of(static_cast<float>(a * (1.0 - kPredEps))))
+        const bool before = a <= top_p * (1.0 + kPredEps);  // acc stops at top_p
+        const bool decides = before && a_end * (1.0 + kPredEps) >= top_p;
+        if (before && ((pw & PF_MUST_A) || decides ||
+                       binade_of(static_cast<float>(a_end * (1.0 + kPredEps))) !=
+                           binade_of(static_cast<float>(a * (1.0 - kPredEps)))))
             set_bit(e_xreq(FK_A), b);
         e_plan()[b] = pw;
     }
@@ -1087,6 +1089,7 @@ __device__ __forceinline__ bool locate(uint32_t lb, uint32_t pos, uint32_t nruns
 }
 
 constexpr uint32_t kHot = 32;  // weight factor of coarse bins where a fold steps value by value
+constexpr uint32_t kFineCap = 1024;  // candidates a fine bin's share of the weight may hold
 
 // Does a coarse bin of approximate mass m after cumulative mass P (of tot)
 // hold a predicted event: total crossing a power of two, acc = total / tot
@@ -1099,9 +1102,12 @@ __device__ __forceinline__ bool coarse_hot(double P, double m, double tot, float
     const double lo = P * (1.0 - kPlanEps), hi = (P + m) * (1.0 + kPlanEps);
     if (!(lo > 0.0) || binade_of(static_cast<float>(lo)) != binade_of(static_cast<float>(hi))) return true;
     if (topp) {
-        if (binade_of(static_cast<float>(lo / tot)) != binade_of(static_cast<float>(hi / tot))) return true;
+        // acc stops at top_p: a bin that starts past it is never walked by acc
         const double tp = static_cast<double>(top_p) * tot;
-        if (lo <= tp && tp <= hi) return true;
+        if (lo <= tp * (1.0 + kPlanEps)) {
+            if (binade_of(static_cast<float>(lo / tot)) != binade_of(static_cast<float>(hi / tot))) return true;
+            if (tp <= hi) return true;
+        }
     }
     if (draw) {
         const double M = topp ? static_cast<double>(top_p) * tot : tot;
@@ -1191,8 +1197,21 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
             const double m0 = e_mass()[2 * tid], m1 = e_mass()[2 * tid + 1];
             double mtot;
             const double P0 = block_excl_scan_f64(m0 + m1, f.miscd() + 8, &mtot);
-            const uint32_t w0c = c0 * (coarse_hot(P0, m0, mtot, u, topp, draw, f.P.top_p) ? kHot : 1u);
-            const uint32_t w1c = c1 * (coarse_hot(P0 + m0, m1, mtot, u, topp, draw, f.P.top_p) ? kHot : 1u);
+            const bool h0 = coarse_hot(P0, m0, mtot, u, topp, draw, f.P.top_p);
+            const bool h1 = coarse_hot(P0 + m0, m1, mtot, u, topp, draw, f.P.top_p);
+            // the hot factor, lowered when hot bins hold most candidates so
+            // that a fine bin (a 1/kNB share of the weight) holds at most
+            // kFineCap candidates, which the census can take
+            const uint32_t hc = block_sum<kBlock>((h0 ? c0 : 0u) + (h1 ? c1 : 0u), f.tmp());
+            uint32_t hot = kHot;
+            if (hc > 0) {
+                const uint64_t room = static_cast<uint64_t>(kNB) * kFineCap;
+                const uint64_t cold = len - hc;
+                const uint64_t k = room > cold ? (room - cold) / hc : 1u;
+                hot = static_cast<uint32_t>(k < 1u ? 1u : (k > kHot ? kHot : k));
+            }
+            const uint32_t w0c = c0 * (h0 ? hot : 1u);
+            const uint32_t w1c = c1 * (h1 ? hot : 1u);
             uint32_t wtot;
             const uint32_t W0 = block_excl_scan<kBlock>(w0c + w1c, f.tmp(), &wtot);
             e_lay()[2 * tid] = W0;

@@ -301,3 +301,102 @@ def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, 
         mask = pack_mask(allowed)
     top_stride = 20 if logprobs else 0
     return Workload(f"rand{seed}", x, vocab, p, ids, offs, mask, uniforms(rng, rows), top_stride=top_stride)
+
+
+# ---- JSON-object constraints (mask producer) ----------------------------------
+
+def _pick_bytes(rng, alphabet, n):
+    """n bytes drawn from `alphabet` (a list of byte values)."""
+    return bytes(np.asarray(rng.choice(alphabet, n), np.uint8).tolist())
+
+
+JSON_FRAGMENTS = [
+    b"{", b"}", b"[", b"]", b",", b":", b'"', b'{"', b'"}', b'":', b'": ', b'", "', b'",', b'"]', b'["',
+    b"[{", b"}]", b"},", b"],", b" {", b" [", b"true", b"false", b"null", b"tru", b"fal", b"nul", b"ue",
+    b"se", b"ll", b"0", b"-", b"-0", b"0.", b".5", b"1e", b"e+", b"E-", b"12", b"123", b"3.14", b"1e10",
+    b"00", b"01", b"-.", b"\\", b"\\n", b'\\"', b"\\u", b"\\u00", b"00e9", b"\\x", b"ab", b" ", b"  ",
+    b"    ", b"\n", b"\n  ", b"\t", b"\r\n", b'  "', b"\xc3\xa9", b"\xe2\x82\xac", b"\x01", b"\x1f",
+    b'{"a', b'"a"', b'": "', b'": [', b'": {', b'": 1', b'": -', b'": t', b'": n', b'": f', b"}}",
+    b"]]", b"},{", b'", "b', b"1,", b"1}", b"0]", b" 1", b" -", b" :", b": ", b" ,", b" }", b" ]",
+]
+
+
+def json_vocab(n_tokens=151936, seed=0x15A0, n_special=24, n_empty=8):
+    """A synthetic tokenizer vocabulary for the mask producer: every single
+    byte, JSON fragments, BPE-like words (letters, digits, punctuation, UTF-8,
+    a leading space), some long tokens, empty tokens and special tokens.
+    Returns (tokens: list of bytes, special_ids)."""
+    rng = np.random.default_rng(seed)
+    toks = [bytes([b]) for b in range(256)] + list(JSON_FRAGMENTS)
+    alpha = b"abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ"
+    punct = b"{}[]:,\"\\-+.eE0123456789 \t\n"
+    while len(toks) < n_tokens - n_special - n_empty:
+        kind = rng.integers(0, 10)
+        if kind < 5:      # a word, often with a leading space
+            w = _pick_bytes(rng, list(alpha), int(rng.integers(1, 10)))
+            toks.append((b" " if rng.random() < 0.5 else b"") + w)
+        elif kind < 7:    # digits and number pieces
+            toks.append(_pick_bytes(rng, list(b"0123456789.eE+-"), int(rng.integers(1, 7))))
+        elif kind < 9:    # punctuation runs, JSON-ish
+            toks.append(_pick_bytes(rng, list(punct), int(rng.integers(1, 5))))
+        else:             # UTF-8 text or a long token
+            if rng.random() < 0.8:
+                cps = rng.integers(0xA0, 0x3000, int(rng.integers(1, 4)))
+                toks.append("".join(chr(int(c)) for c in cps).encode())
+            else:
+                toks.append(_pick_bytes(rng, list(alpha + b" "), int(rng.integers(16, 64))))
+    toks += [b""] * n_empty
+    specials = []
+    for k in range(n_special):
+        specials.append(len(toks))
+        toks.append(b"<|special_%d|>" % k)
+    return toks[:n_tokens], [s for s in specials if s < n_tokens]
+
+
+def json_document(rng, depth=0, max_depth=4):
+    """A random JSON value's bytes (the top level an object)."""
+    def ws():
+        return _pick_bytes(rng, list(b" \n\t"), int(rng.integers(0, 3))) if rng.random() < 0.4 else b""
+
+    def string():
+        parts = []
+        for _ in range(int(rng.integers(0, 6))):
+            r = rng.random()
+            if r < 0.1:
+                parts.append([b'\\"', b"\\\\", b"\\n", b"\\u00e9", b"\\/"][int(rng.integers(0, 5))])
+            elif r < 0.2:
+                parts.append("é€".encode())
+            else:
+                parts.append(_pick_bytes(rng, list(b"abcxyz 0123"), int(rng.integers(1, 5))))
+        return b'"' + b"".join(parts) + b'"'
+
+    def value(d):
+        r = rng.random()
+        if d < max_depth and r < 0.25:
+            return obj(d + 1)
+        if d < max_depth and r < 0.4:
+            items = [ws() + value(d + 1) + ws() for _ in range(int(rng.integers(0, 4)))]
+            return b"[" + b",".join(items) + b"]"
+        if r < 0.6:
+            return string()
+        if r < 0.85:
+            return [b"0", b"-12", b"3.25", b"1e10", b"-0.5E-3", b"42"][int(rng.integers(0, 6))]
+        return [b"true", b"false", b"null"][int(rng.integers(0, 3))]
+
+    def obj(d):
+        items = [ws() + string() + ws() + b":" + ws() + value(d) + ws() for _ in range(int(rng.integers(0, 4)))]
+        return b"{" + b",".join(items) + b"}"
+
+    return obj(depth)
+
+
+def json_prefixes(count, seed=0x15A1):
+    """`count` random cuts of random JSON-object documents (bytes), from the
+    empty prefix to whole documents: the states a constrained sequence
+    passes through."""
+    rng = np.random.default_rng(seed)
+    out = [b""]
+    while len(out) < count:
+        doc = json_document(rng)
+        out.append(doc[:int(rng.integers(0, len(doc) + 1))])
+    return out[:count]

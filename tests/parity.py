@@ -129,6 +129,9 @@ RANDOM_CASES = [
     dict(seed=26, vocab=3000, rows=20, hist_len=4000),
     # penalties over a vocabulary beyond the history bitmap (262144 ids)
     dict(seed=27, vocab=300000, rows=20, hist_len=64),
+    # nucleus rows of ~150k candidates under one dominant value (top-p decided
+    # at the first candidate: value bins past the decision stay coarse)
+    dict(seed=29, vocab=151936, rows=6, mode="nucleus", sigma=3.0, outlier=18.0),
 ]
 
 DIST_CASES = [(21, dict(vocab=500, mode="mixed")), (22, dict(vocab=3000, mode="minp")),

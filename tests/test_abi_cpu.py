@@ -45,17 +45,21 @@ int main(void) {{
   printf("%zu %zu %zu\\n", sizeof(tsm_row_params), sizeof(tsm_batch), sizeof(tsm_outputs));
   printf("%zu %zu %zu %zu\\n", offsetof(tsm_batch, params), offsetof(tsm_batch, uniforms),
          offsetof(tsm_outputs, top_stride), offsetof(tsm_outputs, keep));
+  printf("%zu %zu %zu %zu\\n", sizeof(tsm_json_state), offsetof(tsm_json_state, whitespace),
+         sizeof(tsm_vocab), offsetof(tsm_vocab, n_tokens));
   return 0;
 }}''')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", str(src), "-o", str(exe)], check=True)
-    l1, l2 = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")[:2]
+    l1, l2, l3 = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")[:3]
     from tachyon_amd.workloads import ROW_PARAMS_DTYPE
 
     assert [int(v) for v in l1.split()] == [ROW_PARAMS_DTYPE.itemsize, ctypes.sizeof(_lib.TsmBatch),
                                             ctypes.sizeof(_lib.TsmOutputs)]
     assert [int(v) for v in l2.split()] == [_lib.TsmBatch.params.offset, _lib.TsmBatch.uniforms.offset,
                                             _lib.TsmOutputs.top_stride.offset, _lib.TsmOutputs.keep.offset]
+    assert [int(v) for v in l3.split()] == [ctypes.sizeof(_lib.TsmJsonState), _lib.TsmJsonState.whitespace.offset,
+                                            ctypes.sizeof(_lib.TsmVocab), _lib.TsmVocab.n_tokens.offset]
 
 
 def _no_gpu():
@@ -87,3 +91,10 @@ def test_argument_errors_need_no_device():
     assert L.tsm_distribution(None, None, None, None, None, 0, None, err, len(err)) != 0
     assert L.tsm_status(None, None, err, len(err)) != 0
     L.tsm_destroy(None)
+    # the mask producer checks its arguments on the host before any launch
+    assert L.tsm_json_mask(None, None, None, 1, 10, None, 1, err, len(err)) != 0
+    assert b"vocab" in err.value
+    v = _lib.TsmVocab(None, None, None, 0, 0)
+    st = _lib.TsmJsonState()
+    assert L.tsm_json_mask(None, ctypes.byref(v), ctypes.byref(st), 1, 100, ctypes.byref(st), 1, err, len(err)) != 0
+    assert b"mask_stride" in err.value

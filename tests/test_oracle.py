@@ -461,3 +461,59 @@ def test_nan_and_inf_semantics_hand_derived(oracle):
     # a NaN at id 0 and greedy: argmax returns 0 whatever follows
     r = one([nan, 9.0, 1.0], temperature=0.0)
     assert r.token[0] == 0
+
+
+# ---- JsonObject (constrain.rs), the mask producer's oracle -------------------
+
+JSON_VALID = [  # constrain.rs:315-326: accepted and complete
+    b'{}',
+    b'{"a": 1}',
+    b'{"name": "Ada", "age": 36, "langs": ["en", "fr"], "ok": true, "x": null}',
+    '{"n": -0.5e+10, "z": 0, "e": "é\\n\\"q\\""}'.encode(),
+    b'{\n  "nested": {"deep": [[1, 2], {"k": false}]}\n}',
+]
+JSON_PREFIXES = [  # constrain.rs:329-340: accepted, not complete
+    b'{"a": "unfinished',
+    b'{"a": [1, 2',
+    b'{"a": tr',
+    b'{"a": 12',
+]
+JSON_INVALID = [  # constrain.rs:343-361: rejected
+    b"[1]", b'"top"', b"{a: 1}", b'{"a" 1}', b'{"a": 01}', b'{"a": 1,}', b'{"a": tru}', b'{"a": "\\x"}',
+    b'{"a": [1}', b'{"a": 1}}', b'{"a": "line\nbreak"}', b'{"a": .5}',
+]
+
+
+def test_json_reference_tests(oracle):
+    """The reference's own constraint tests (constrain.rs:304-362)."""
+    for t in JSON_VALID:
+        assert oracle.json_check(t) == (True, True), t
+    for t in JSON_PREFIXES:
+        assert oracle.json_check(t) == (True, False), t
+    for t in JSON_INVALID:
+        assert not oracle.json_check(t)[0], t
+    assert not oracle.json_check(b"{" + b" " * 40)[0]  # whitespace_is_bounded
+
+
+def test_json_limits_hand_derived(oracle):
+    """Limits traced through constrain.rs: a number's step returns `len < 40`
+    with the length before the byte (the first digit is length 1), so 40
+    digits pass and the 41st fails; `open` refuses a 33rd container; 16
+    whitespace bytes in a row pass and the 17th fails; \\u takes exactly four
+    hex digits."""
+    assert oracle.json_check(b'{"a": ' + b"1" * 40)[0]
+    assert not oracle.json_check(b'{"a": ' + b"1" * 41)[0]
+    deep = b'{"a":' + b"[" * 31
+    assert oracle.json_check(deep)[0]
+    assert not oracle.json_check(deep + b"[")[0]
+    assert oracle.json_check(b"{" + b" " * 16)[0]
+    assert not oracle.json_check(b"{" + b" " * 17)[0]
+    assert oracle.json_check(b'{"a": "\\u00e9"}') == (True, True)
+    assert not oracle.json_check(b'{"a": "\\u00g9"}')[0]
+    # a number ends at a byte that cannot continue it, which then counts as structure
+    assert oracle.json_check(b'{"a": 0}') == (True, True)
+    assert oracle.json_check(b'{"a": -0.5e-3 }') == (True, True)
+    assert not oracle.json_check(b'{"a": -}')[0]
+    assert not oracle.json_check(b'{"a": 1.}')[0]
+    # after the object closes nothing follows, not even whitespace
+    assert not oracle.json_check(b"{} ")[0]
