@@ -116,6 +116,7 @@ enum : uint32_t {  // e_sc() words
     SC_X = 11,
     SC_OVF = 12,    // census table full
     SC_CMIN = 13,   // smallest candidate value's total key
+    SC_TIED = 14,   // walk: a bin sum it added holds a tie
 };
 
 // Grid plan of a bin, one byte per fold for the lower grid's binade (+128)
@@ -400,6 +401,7 @@ struct Walk {
     uint32_t pos;     // candidates folded so far
     uint32_t run;     // W_DECIDED: the deciding run and the index within it
     uint32_t within;
+    uint32_t tied;    // a bound walk added a bin sum holding a tie (else its result is exact)
 };
 
 // The runs [r0, r1) of one bin, in order, folding at most up to candidate
@@ -516,7 +518,7 @@ __device__ uint32_t walk_bins(Walk& w, uint32_t bend, uint32_t nruns, float T, f
             const uint32_t bl = w.b + kBL * lane;
             uint32_t nj[kBL], cj[kBL];
             bool okj[kBL];
-            uint32_t ln = 0, lc = 0;
+            uint32_t ln = 0, lc = 0, tmask = 0;  // tmask: the lane's summable bins holding a tie
 #pragma unroll
             for (uint32_t j = 0; j < kBL; j++) {
                 const uint32_t b = bl + j;
@@ -537,7 +539,11 @@ __device__ uint32_t walk_bins(Walk& w, uint32_t bend, uint32_t nruns, float T, f
                         // take its lower (kB 1) or upper (kB 2) end
                         ok = slot != 0xFFFFFFFFu && b != force &&
                              (kB == 0 ? !tie_bit(slot, b) : !bad_bit(slot, b));
-                        if (ok) c = static_cast<uint64_t>(e_sum(slot)[b]) + (kB == 2 && tie_bit(slot, b) ? 1u : 0u);
+                        if (ok) {
+                            const bool tie = kB != 0 && tie_bit(slot, b);
+                            c = static_cast<uint64_t>(e_sum(slot)[b]) + (kB == 2 && tie ? 1u : 0u);
+                            if (tie) tmask |= 1u << j;
+                        }
                     }
                 }
                 // past 2^25 units a bin leaves the binade anyway: the clamps keep
@@ -588,6 +594,10 @@ __device__ uint32_t walk_bins(Walk& w, uint32_t bend, uint32_t nruns, float T, f
                 np += nj[j];
             }
             const uint32_t f = first_lane(wave_ballot(jb < kBL));
+            if (kB != 0) {  // the bins added below: every bin of the lanes before f, lane f's before jb
+                const uint32_t applied = lane < f ? tmask : (lane == f ? tmask & ((1u << jb) - 1u) : 0u);
+                if (wave_ballot(applied != 0u)) w.tied = 1u;
+            }
             // lanes after f recorded bin starts past the stop; the next step
             // writes them again from the right value
             if (f == 64u) {
@@ -1032,6 +1042,7 @@ __device__ __noinline__ uint32_t run_walk(Fin& f_in, const Filt& q_in, const FBi
                 e_sc()[SC_RUN] = w.run;
                 e_sc()[SC_WITHIN] = w.within;
                 e_sc()[SC_X] = __float_as_uint(w.x);
+                e_sc()[SC_TIED] = w.tied;
             }
         }
         TSM_LDS_SYNC();
@@ -1041,6 +1052,7 @@ __device__ __noinline__ uint32_t run_walk(Fin& f_in, const Filt& q_in, const FBi
         w.run = e_sc()[SC_RUN];
         w.within = e_sc()[SC_WITHIN];
         w.x = __uint_as_float(e_sc()[SC_X]);
+        w.tied = e_sc()[SC_TIED];
         TSM_LDS_SYNC();
         if (res != W_NEED) {
             w_io = w;
@@ -1274,7 +1286,7 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     w0.x = 0.0f;
     w0.b = 0;
     w0.pos = 0;
-    w0.run = w0.within = 0;
+    w0.run = w0.within = w0.tied = 0;
     // total: with every unresolved tie rounded down, then up; when both give
     // the same value it is total (the fold is monotone in each step), else
     // the ties are censused and stepped exactly
@@ -1282,7 +1294,16 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     {
         Walk wl = w0, wh = w0;
         if (run_walk<FK_S, 1>(f, q, vb, wl, kNB, 0.0f, 0.0f, kNoBin, 0xFFFFFFFFu, draw, topp) == W_NEED) return out;
-        if (run_walk<FK_S, 2>(f, q, vb, wh, kNB, 0.0f, 0.0f, kNoBin, 0xFFFFFFFFu, draw, topp) == W_NEED) return out;
+        if (wl.tied) {
+            if (run_walk<FK_S, 2>(f, q, vb, wh, kNB, 0.0f, 0.0f, kNoBin, 0xFFFFFFFFu, draw, topp) == W_NEED)
+                return out;
+        } else {
+            // no bin sum it added held a tie: every step was exact, and so is
+            // every bin start it recorded
+            wh = wl;
+            for (uint32_t b = tid; b < kNB; b += kBlock) e_shi()[b] = e_sstart()[b];
+            TSM_LDS_SYNC();
+        }
         T = wl.x;
         if (__float_as_uint(wl.x) != __float_as_uint(wh.x)) {
             // the exact walk from the last bin where both walks still agree
@@ -1310,8 +1331,13 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
         Walk wal = w0, wa = w0;
         const uint32_t ral = run_walk<FK_A, 1>(f, q, vb, wal, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
         if (ral == W_NEED) return out;
-        uint32_t ra = run_walk<FK_A, 2>(f, q, vb, wa, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
-        if (ra == W_NEED) return out;
+        uint32_t ra = ral;
+        if (wal.tied) {
+            ra = run_walk<FK_A, 2>(f, q, vb, wa, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
+            if (ra == W_NEED) return out;
+        } else {
+            wa = wal;  // exact: no tie in any bin sum it added
+        }
         if (ra != ral || (ra == W_DECIDED && wa.pos != wal.pos)) {
             wa = w0;
             ra = run_walk<FK_A>(f, q, vb, wa, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
@@ -1347,6 +1373,7 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
             }
             if (tid < kWave) {  // the kept mass: total's fold through the kept part of bin kb
                 Walk wm;
+                wm.tied = 0;
                 wm.x = e_sstart()[kb];
                 wm.b = kb;
                 wm.pos = e_pstart()[kb];
@@ -1385,15 +1412,20 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     wr.x = u * mass;
     wr.b = 0;
     wr.pos = 0;
-    wr.run = wr.within = 0;
+    wr.run = wr.within = wr.tied = 0;
     const uint32_t bend = kb != kNoBin ? kb + 1u : kNB;
     // the draw with unresolved ties one way, then the other; the same pick
     // from both is the draw's, else the exact walk
     Walk wrl = wr;
     const uint32_t rrl = run_walk<FK_R, 1>(f, q, vb, wrl, bend, 0.0f, 0.0f, kb, keep, draw, false);
     if (rrl == W_NEED) return out;
-    uint32_t rr = run_walk<FK_R, 2>(f, q, vb, wr, bend, 0.0f, 0.0f, kb, keep, draw, false);
-    if (rr == W_NEED) return out;
+    uint32_t rr = rrl;
+    if (wrl.tied) {
+        rr = run_walk<FK_R, 2>(f, q, vb, wr, bend, 0.0f, 0.0f, kb, keep, draw, false);
+        if (rr == W_NEED) return out;
+    } else {
+        wr = wrl;  // exact: no tie in any bin sum it added
+    }
     if (rr != rrl || (rr == W_DECIDED && wr.pos != wrl.pos)) {
         wr = wrl;
         wr.x = u * mass;
