@@ -500,7 +500,7 @@ __device__ uint32_t walk_bins(Walk& w, uint32_t bend, uint32_t nruns, float T, f
             if (K == FK_S && b < bend && lane <= f) {
                 if (kB != 2) e_sstart()[b] = 0.0f;
                 if (kB != 1) e_shi()[b] = 0.0f;
-                e_pstart()[b] = w.pos;
+                if (kB != 2) e_pstart()[b] = w.pos;  // the ties-up walk runs beside the ties-down one
             }
             if (f == 64u) {
                 w.b += 64u;
@@ -581,7 +581,7 @@ __device__ uint32_t walk_bins(Walk& w, uint32_t bend, uint32_t nruns, float T, f
                         const float sv = ldexpf(static_cast<float>(start), g);
                         if (kB != 2) e_sstart()[bl + j] = sv;
                         if (kB != 1) e_shi()[bl + j] = sv;
-                        e_pstart()[bl + j] = w.pos + np;
+                        if (kB != 2) e_pstart()[bl + j] = w.pos + np;
                     }
                     if (bad) {
                         jb = j;
@@ -1082,6 +1082,95 @@ __device__ __noinline__ uint32_t run_walk(Fin& f_in, const Filt& q_in, const FBi
     }
 }
 
+// Fold K's two bound walks at once: ties down (kB 1) on wave 0 from wl, ties
+// up (kB 2) on wave 1 from wh, with shared census rounds wherever either
+// lacks a bin.  The walks read the same sums and census and write their own
+// bin-start records (e_sstart, e_shi; e_pstart gets the same positions from
+// both).  Sets *rl and *rh; returns W_NEED when a bin holds more distinct
+// values than the census, else W_DONE.
+constexpr uint32_t kSc2 = 16;  // e_sc() words 16..29: the two walks' results, 7 words each
+template <int K>
+__device__ __noinline__ uint32_t run_walk2(Fin& f_in, const Filt& q_in, const FBins& vb_in, Walk& wl_io,
+                                           Walk& wh_io, uint32_t* rl, uint32_t* rh, uint32_t bend, float T,
+                                           float thr, uint32_t force, uint32_t lim, bool draw, bool acc_next) {
+    Fin f = f_in;  // a private copy: its fields stay in registers across LDS atomics
+    const Filt q = q_in;
+    const FBins vb = vb_in;
+    const uint32_t tid = threadIdx.x, wid = tid / kWave;
+    Walk w0 = wl_io, w1 = wh_io;
+    uint32_t r0 = W_NEED, r1 = W_NEED;
+    uint32_t from0 = kNoBin, from1 = kNoBin;  // the bin each walk last asked the census for
+    bool alone = false;
+    for (;;) {
+        const uint32_t nruns = e_sc()[SC_NRUNS];
+        if (wid < 2u && (wid == 0u ? r0 : r1) == W_NEED) {
+            Walk w = wid == 0u ? w0 : w1;
+            const uint32_t res = wid == 0u ? walk_bins<K, 1>(w, bend, nruns, T, thr, force, lim)
+                                           : walk_bins<K, 2>(w, bend, nruns, T, thr, force, lim);
+            if (lane_id() == 0) {
+                uint32_t* o = e_sc() + kSc2 + 7u * wid;
+                o[0] = res;
+                o[1] = w.b;
+                o[2] = w.pos;
+                o[3] = w.run;
+                o[4] = w.within;
+                o[5] = __float_as_uint(w.x);
+                o[6] = w.tied;
+            }
+        }
+        TSM_LDS_SYNC();
+#pragma unroll
+        for (uint32_t j = 0; j < 2u; j++) {
+            if ((j == 0u ? r0 : r1) != W_NEED) continue;
+            const uint32_t* o = e_sc() + kSc2 + 7u * j;
+            Walk& w = j == 0u ? w0 : w1;
+            w.b = o[1];
+            w.pos = o[2];
+            w.run = o[3];
+            w.within = o[4];
+            w.x = __uint_as_float(o[5]);
+            w.tied = o[6];
+            if (j == 0u) r0 = o[0];
+            else r1 = o[0];
+        }
+        TSM_LDS_SYNC();
+        if (r0 != W_NEED && r1 != W_NEED) break;
+        // a census round from the lower of the bins the walks stopped at; a
+        // walk that stops again at the bin it last asked for gets that bin
+        // alone, once
+        const bool n0 = r0 == W_NEED, n1 = r1 == W_NEED;
+        const uint32_t b = n0 && n1 ? min(w0.b, w1.b) : (n0 ? w0.b : w1.b);
+        const bool again = (n0 && w0.b == b && from0 == b) || (n1 && w1.b == b && from1 == b);
+        if (again) {
+            if (alone) {
+                wl_io = w0;
+                wh_io = w1;
+                *rl = r0;
+                *rh = r1;
+                return W_NEED;
+            }
+            alone = true;
+            if (tid < kNB / 32u) e_req()[tid] = 0u;
+            TSM_LDS_SYNC();
+            if (tid == 0) set_bit(e_req(), b);
+            TSM_LDS_SYNC();
+        } else {
+            alone = false;
+            request_round(K, b, draw, acc_next, false, true);
+        }
+        if (n0 && w0.b == b) from0 = b;
+        if (n1 && w1.b == b) from1 = b;
+        census_clear();
+        eng_pass<EP_CENSUS>(f, q, vb, 0.0f);
+        census_finish(vb, f.m.t);
+    }
+    wl_io = w0;
+    wh_io = w1;
+    *rl = r0;
+    *rh = r1;
+    return W_DONE;
+}
+
 // The kept candidate at position pos (0-based, pos < kept count) when no step
 // of the draw decides: its run and index within the run, from bin lb's runs.
 __device__ __forceinline__ bool locate(uint32_t lb, uint32_t pos, uint32_t nruns, uint32_t* run, uint32_t* within) {
@@ -1293,17 +1382,9 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     float T;
     {
         Walk wl = w0, wh = w0;
-        if (run_walk<FK_S, 1>(f, q, vb, wl, kNB, 0.0f, 0.0f, kNoBin, 0xFFFFFFFFu, draw, topp) == W_NEED) return out;
-        if (wl.tied) {
-            if (run_walk<FK_S, 2>(f, q, vb, wh, kNB, 0.0f, 0.0f, kNoBin, 0xFFFFFFFFu, draw, topp) == W_NEED)
-                return out;
-        } else {
-            // no bin sum it added held a tie: every step was exact, and so is
-            // every bin start it recorded
-            wh = wl;
-            for (uint32_t b = tid; b < kNB; b += kBlock) e_shi()[b] = e_sstart()[b];
-            TSM_LDS_SYNC();
-        }
+        uint32_t rl, rh;
+        if (run_walk2<FK_S>(f, q, vb, wl, wh, &rl, &rh, kNB, 0.0f, 0.0f, kNoBin, 0xFFFFFFFFu, draw, topp) == W_NEED)
+            return out;
         T = wl.x;
         if (__float_as_uint(wl.x) != __float_as_uint(wh.x)) {
             // the exact walk from the last bin where both walks still agree
@@ -1326,18 +1407,13 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
         census_clear();
         eng_pass<EP_A>(f, q, vb, T);
         census_finish(vb, t);
-        // acc the same way: ties down, then up; the same decision from both
+        // acc the same way: ties down and up at once; the same decision from both
         // is acc's, else the exact walk
         Walk wal = w0, wa = w0;
-        const uint32_t ral = run_walk<FK_A, 1>(f, q, vb, wal, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
-        if (ral == W_NEED) return out;
-        uint32_t ra = ral;
-        if (wal.tied) {
-            ra = run_walk<FK_A, 2>(f, q, vb, wa, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
-            if (ra == W_NEED) return out;
-        } else {
-            wa = wal;  // exact: no tie in any bin sum it added
-        }
+        uint32_t ral, ra;
+        if (run_walk2<FK_A>(f, q, vb, wal, wa, &ral, &ra, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false) ==
+            W_NEED)
+            return out;
         if (ra != ral || (ra == W_DECIDED && wa.pos != wal.pos)) {
             wa = w0;
             ra = run_walk<FK_A>(f, q, vb, wa, kNB, T, f.P.top_p, kNoBin, 0xFFFFFFFFu, draw, false);
@@ -1414,18 +1490,11 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     wr.pos = 0;
     wr.run = wr.within = wr.tied = 0;
     const uint32_t bend = kb != kNoBin ? kb + 1u : kNB;
-    // the draw with unresolved ties one way, then the other; the same pick
+    // the draw with unresolved ties one way and the other at once; the same pick
     // from both is the draw's, else the exact walk
     Walk wrl = wr;
-    const uint32_t rrl = run_walk<FK_R, 1>(f, q, vb, wrl, bend, 0.0f, 0.0f, kb, keep, draw, false);
-    if (rrl == W_NEED) return out;
-    uint32_t rr = rrl;
-    if (wrl.tied) {
-        rr = run_walk<FK_R, 2>(f, q, vb, wr, bend, 0.0f, 0.0f, kb, keep, draw, false);
-        if (rr == W_NEED) return out;
-    } else {
-        wr = wrl;  // exact: no tie in any bin sum it added
-    }
+    uint32_t rrl, rr;
+    if (run_walk2<FK_R>(f, q, vb, wrl, wr, &rrl, &rr, bend, 0.0f, 0.0f, kb, keep, draw, false) == W_NEED) return out;
     if (rr != rrl || (rr == W_DECIDED && wr.pos != wrl.pos)) {
         wr = wrl;
         wr.x = u * mass;
