@@ -339,4 +339,76 @@ std::vector<std::vector<std::pair<uint32_t, float>>> BatchSampler::distribution(
     return out;
 }
 
+// ---- constrained decoding: JsonObject ---------------------------------------------
+
+JsonObjectConstraint::JsonObjectConstraint() { tsm_json_init(&s_); }
+
+bool JsonObjectConstraint::allows(const Vocab& v, uint32_t token) const {
+    if (token >= v.tokens.size()) return false;  // token_bytes: empty past the table
+    if (token < v.special.size() && v.special[token]) return false;
+    const auto& b = v.tokens[token];
+    return !b.empty() && tsm_json_accepts(&s_, b.data(), b.size()) != 0;
+}
+
+bool JsonObjectConstraint::accepts(const uint8_t* bytes, size_t n) const { return tsm_json_accepts(&s_, bytes, n) != 0; }
+
+void JsonObjectConstraint::advance(const uint8_t* bytes, size_t n) { tsm_json_advance(&s_, bytes, n); }
+
+bool JsonObjectConstraint::is_complete() const { return tsm_json_is_complete(&s_) != 0; }
+
+DeviceVocab::DeviceVocab(int device, const Vocab& v, uint32_t max_rows) : device_(device), max_rows_(max_rows) {
+    const size_t n = v.tokens.size();
+    std::vector<uint32_t> offsets(n + 1, 0);
+    for (size_t i = 0; i < n; i++) offsets[i + 1] = offsets[i] + static_cast<uint32_t>(v.tokens[i].size());
+    std::vector<uint8_t> bytes(offsets[n] ? offsets[n] : 1u, 0);
+    for (size_t i = 0; i < n; i++)
+        if (!v.tokens[i].empty()) std::memcpy(bytes.data() + offsets[i], v.tokens[i].data(), v.tokens[i].size());
+    std::vector<uint32_t> special((n + 31) / 32 + 1, 0u);
+    for (size_t i = 0; i < n && i < v.special.size(); i++)
+        if (v.special[i]) special[i >> 5] |= 1u << (i & 31u);
+    const size_t ob = offsets.size() * 4, sb = special.size() * 4, bb = bytes.size();
+    const size_t stb = (static_cast<size_t>(max_rows_) * sizeof(tsm_json_state) + 255) / 256 * 256;
+    int prev = 0;
+    check(hipGetDevice(&prev), "hipGetDevice");
+    check(hipSetDevice(device_), "hipSetDevice");
+    hipError_t e = hipMalloc(&mem_, stb + ob + sb + bb);
+    states_ = static_cast<tsm_json_state*>(mem_);
+    char* p = static_cast<char*>(mem_) + stb;
+    if (e == hipSuccess) e = hipMemcpy(p, offsets.data(), ob, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p + ob, special.data(), sb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p + ob + sb, bytes.data(), bb, hipMemcpyHostToDevice);
+    (void)hipSetDevice(prev);
+    check(e, "DeviceVocab upload");
+    abi_.offsets = reinterpret_cast<const uint32_t*>(p);
+    abi_.special = reinterpret_cast<const uint32_t*>(p + ob);
+    abi_.bytes = reinterpret_cast<const uint8_t*>(p + ob + sb);
+    abi_.n_tokens = static_cast<uint32_t>(n);
+    abi_.reserved = 0;
+}
+
+DeviceVocab::~DeviceVocab() {
+    if (mem_) (void)hipFree(mem_);
+}
+
+void DeviceVocab::json_masks(const std::vector<const JsonObjectConstraint*>& rows, uint32_t usable, uint32_t* mask,
+                             uint32_t mask_stride, void* stream) {
+    if (rows.empty()) return;
+    if (rows.size() > max_rows_)
+        throw Error("json_masks: " + std::to_string(rows.size()) + " rows exceed the vocabulary's max_rows " +
+                    std::to_string(max_rows_));
+    std::vector<tsm_json_state> states(rows.size());
+    for (size_t r = 0; r < rows.size(); r++) {
+        if (!rows[r]) throw Error("json_masks: a row has no constraint");
+        states[r] = rows[r]->state();
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    check(hipMemcpyAsync(states_, states.data(), states.size() * sizeof(tsm_json_state), hipMemcpyHostToDevice, s),
+          "json_masks upload");
+    char err[256] = {0};
+    const int rc = tsm_json_mask(stream, &abi_, states_, static_cast<uint32_t>(rows.size()), usable, mask,
+                                 mask_stride, err, sizeof(err));
+    check(hipStreamSynchronize(s), "json_masks");  // `states` is read by the copy until then
+    if (rc != 0) throw Error(err);
+}
+
 }  // namespace tachyon

@@ -17,6 +17,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -145,6 +146,58 @@ class BatchSampler {
     uint32_t last_status_ = 0;
     tsm_ctx* ctx_ = nullptr;
     Staging* st_ = nullptr;
+};
+
+// ---- constrained decoding: JsonObject (src/constrain.rs) -----------------------
+
+// A tokenizer's token bytes and special flags on the host (tokenizer.rs:
+// 189-195: token_bytes, is_special).
+struct Vocab {
+    std::vector<std::vector<uint8_t>> tokens;
+    std::vector<bool> special;  // empty or one flag per token
+};
+
+// The Constraint for `response_format: json_object` (constrain.rs:14-42,
+// 88-302), on the packed state the GPU mask producer reads.
+class JsonObjectConstraint {
+  public:
+    JsonObjectConstraint();                       // JsonObject::default()
+    // Constraint::allows (constrain.rs:286-290) for one token, on the host.
+    bool allows(const Vocab& v, uint32_t token) const;
+    bool accepts(const uint8_t* bytes, size_t n) const;  // accepts_bytes
+    void advance(const uint8_t* bytes, size_t n);        // Constraint::advance
+    bool is_complete() const;                            // Constraint::is_complete
+    const tsm_json_state& state() const { return s_; }
+
+  private:
+    tsm_json_state s_;
+};
+
+// The vocabulary in device memory for the mask producer, uploaded once, with
+// room for the states of up to max_rows constrained rows (a step allocates
+// nothing).
+class DeviceVocab {
+  public:
+    DeviceVocab(int device, const Vocab& v, uint32_t max_rows = 1024);
+    ~DeviceVocab();
+    DeviceVocab(const DeviceVocab&) = delete;
+    DeviceVocab& operator=(const DeviceVocab&) = delete;
+    const tsm_vocab& abi() const { return abi_; }
+    uint32_t size() const { return abi_.n_tokens; }
+
+    // The allow-bits of a step's constrained rows, every token at once on the
+    // GPU (tsm_json_mask): row r of `mask` (DEVICE, [rows][mask_stride]
+    // words) gets rows[r]'s allows() for ids [0, usable), the layout
+    // BatchSampler::sample takes.  Waits for the masks.
+    void json_masks(const std::vector<const JsonObjectConstraint*>& rows, uint32_t usable, uint32_t* mask,
+                    uint32_t mask_stride, void* stream = nullptr);
+
+  private:
+    int device_;
+    uint32_t max_rows_;
+    tsm_vocab abi_{};
+    void* mem_ = nullptr;
+    tsm_json_state* states_ = nullptr;  // device, [max_rows]
 };
 
 }  // namespace tachyon

@@ -351,6 +351,104 @@ void errors_are_reported(BatchSampler& bs) {
 
 }  // namespace
 
+// ---- JsonObject constraint (constrain.rs) ------------------------------------
+
+static std::vector<uint8_t> bytes_of(const std::string& t) { return std::vector<uint8_t>(t.begin(), t.end()); }
+
+static std::pair<bool, bool> json_check(const std::string& t) {
+    JsonObjectConstraint c;
+    const auto b = bytes_of(t);
+    const bool ok = c.accepts(b.data(), b.size());
+    c.advance(b.data(), b.size());
+    return {ok, c.is_complete()};
+}
+
+// The reference's constraint tests (constrain.rs:313-362) on the C++ API.
+static void json_reference_tests() {
+    for (const char* t : {"{}", "{\"a\": 1}",
+                          "{\"name\": \"Ada\", \"age\": 36, \"langs\": [\"en\", \"fr\"], \"ok\": true, \"x\": null}",
+                          "{\"n\": -0.5e+10, \"z\": 0, \"e\": \"\xc3\xa9\\n\\\"q\\\"\"}",
+                          "{\n  \"nested\": {\"deep\": [[1, 2], {\"k\": false}]}\n}"}) {
+        const auto r = json_check(t);
+        EXPECT(r.first && r.second, "valid: %s", t);
+    }
+    for (const char* t : {"{\"a\": \"unfinished", "{\"a\": [1, 2", "{\"a\": tr", "{\"a\": 12"}) {
+        const auto r = json_check(t);
+        EXPECT(r.first && !r.second, "prefix: %s", t);
+    }
+    for (const char* t : {"[1]", "\"top\"", "{a: 1}", "{\"a\" 1}", "{\"a\": 01}", "{\"a\": 1,}", "{\"a\": tru}",
+                          "{\"a\": \"\\x\"}", "{\"a\": [1}", "{\"a\": 1}}", "{\"a\": \"line\nbreak\"}",
+                          "{\"a\": .5}"}) {
+        EXPECT(!json_check(t).first, "invalid accepted: %s", t);
+    }
+    EXPECT(!json_check("{" + std::string(40, ' ')).first, "whitespace is bounded");
+}
+
+// Constrained generation through the batched path: each step the masks of
+// four JSON-object sequences come from the GPU producer and must equal the
+// host automaton's allows() bit for bit; every pick is allowed, is the
+// oracle's sample_with() under the same mask, and advances its constraint.
+static void json_constrained_generation(BatchSampler& bs) {
+    Vocab v;
+    for (int b = 0; b < 256; b++) v.tokens.push_back({static_cast<uint8_t>(b)});
+    for (const char* t : {"{", "}", "{\"", "\":", "\": ", "\", \"", "\"}", "[", "]", "true", "false", "null",
+                          "12", "-0.5", "e+3", " ", "\n  ", "\"name", "\"a\"", ": [", "],", "\\n", "\\u00e9", "ab"})
+        v.tokens.push_back(bytes_of(t));
+    v.tokens.push_back({});               // an empty token: never allowed
+    v.tokens.push_back(bytes_of("<|x|>")); // a special token: never allowed
+    v.special.assign(v.tokens.size(), false);
+    v.special.back() = true;
+    const uint32_t V = static_cast<uint32_t>(v.tokens.size()), words = (V + 31) / 32, rows = 4;
+    DeviceVocab dv(0, v, rows);
+    std::vector<JsonObjectConstraint> cs(rows);
+    std::vector<Sampler> ss;
+    std::vector<or_sampler*> os;
+    for (uint32_t r = 0; r < rows; r++) {
+        SamplerConfig c = cfg(1.0f, r % 2 ? 0 : 8, 0.95f, 1.0f, 77 + r);
+        ss.emplace_back(c);
+        or_config oc = ocfg(c);
+        os.push_back(or_sampler_new(&oc));
+    }
+    uint32_t* dmask = nullptr;
+    EXPECT(hipMalloc(&dmask, rows * words * 4) == hipSuccess, "hipMalloc");
+    std::mt19937 g(5);
+    std::normal_distribution<float> nd(0.0f, 2.0f);
+    int done = 0;
+    for (int step = 0; step < 40; step++) {
+        std::vector<const JsonObjectConstraint*> cp;
+        for (auto& c : cs) cp.push_back(&c);
+        dv.json_masks(cp, V, dmask, words);
+        std::vector<uint32_t> mask(rows * words);
+        EXPECT(hipMemcpy(mask.data(), dmask, mask.size() * 4, hipMemcpyDeviceToHost) == hipSuccess, "copy");
+        for (uint32_t r = 0; r < rows; r++)
+            for (uint32_t t = 0; t < V; t++)
+                EXPECT(((mask[r * words + t / 32] >> (t % 32)) & 1u) == (cs[r].allows(v, t) ? 1u : 0u),
+                       "step %d row %u token %u: mask bit differs from allows()", step, r, t);
+        std::vector<float> logits(static_cast<size_t>(rows) * V);
+        for (auto& x : logits) x = nd(g);
+        std::vector<RowRequest> req(rows);
+        for (uint32_t r = 0; r < rows; r++) {
+            req[r].sampler = &ss[r];
+            req[r].constrained = true;
+        }
+        float* dl = to_device(logits);
+        const auto tok = bs.sample(dl, rows, V, V, req, dmask, words);
+        (void)hipFree(dl);
+        for (uint32_t r = 0; r < rows; r++) {
+            const uint32_t want = or_sample_with(os[r], logits.data() + static_cast<size_t>(r) * V, V, V, nullptr, 0,
+                                                 mask.data() + r * words);
+            EXPECT(tok[r] == want, "step %d row %u: token %u, oracle %u", step, r, tok[r], want);
+            if (cs[r].is_complete()) continue;  // the object closed: nothing is allowed any more
+            EXPECT(cs[r].allows(v, tok[r]), "step %d row %u: token %u not allowed", step, r, tok[r]);
+            cs[r].advance(v.tokens[tok[r]].data(), v.tokens[tok[r]].size());
+            if (cs[r].is_complete()) done++;
+        }
+    }
+    (void)hipFree(dmask);
+    for (auto* o : os) or_sampler_free(o);
+    std::printf("  %d of %u sequences closed their object\n", done, rows);
+}
+
 int main(int argc, char** argv) {
     const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
     run("rng_matches_the_oracle", rng_matches_the_oracle);
@@ -359,6 +457,7 @@ int main(int argc, char** argv) {
     run("speculative_sampling_preserves_the_target_distribution",
         speculative_sampling_preserves_the_target_distribution);
     run("deterministic_drafts_reduce_to_greedy", deterministic_drafts_reduce_to_greedy);
+    run("json_reference_tests", json_reference_tests);
     if (!cpu_only) {
         BatchSampler bs(0, 16, 8192, 128);
         run("greedy_and_top_k", [&] { greedy_and_top_k(bs); });
@@ -368,6 +467,7 @@ int main(int argc, char** argv) {
         run("penalty_can_flip_the_choice", [&] { penalty_can_flip_the_choice(bs); });
         run("sequences_match_the_oracle", [&] { sequences_match_the_oracle(bs); });
         run("errors_are_reported", [&] { errors_are_reported(bs); });
+        run("json_constrained_generation", [&] { json_constrained_generation(bs); });
     }
     std::printf("%s: %d failed\n", g_failed ? "FAILED" : "OK", g_failed);
     return g_failed ? 1 : 0;
