@@ -58,8 +58,8 @@ __host__ __device__ inline bool is_digit(uint8_t b) { return b >= '0' && b <= '9
 __host__ __device__ inline bool is_hex(uint8_t b) {
     return is_digit(b) || (b >= 'a' && b <= 'f') || (b >= 'A' && b <= 'F');
 }
-// The top container: 1 object, 0 array (depth > 0).
-__host__ __device__ inline uint32_t top(const tsm_json_state& s) { return (s.stack >> (s.depth - 1u)) & 1u; }
+// The top container: 1 object, 0 array (depth in [1, 32]).
+__host__ __device__ inline uint32_t top(const tsm_json_state& s) { return (s.stack >> ((s.depth - 1u) & 31u)) & 1u; }
 
 __host__ __device__ inline void value_done(tsm_json_state& s) { s.state = s.depth == 0 ? JS_DONE : JS_AFTER; }
 
@@ -155,6 +155,7 @@ __host__ __device__ inline bool step(tsm_json_state& s, uint8_t b) {
     } else if (s.state == JS_LITERAL) {
         const char* word = s.aux == 0 ? "true" : s.aux == 1 ? "false" : "null";
         const uint8_t wlen = s.aux == 1 ? 5 : 4;
+        if (s.len >= wlen) return false;  // not a state step() makes: the word's end is not read past
         if (static_cast<uint8_t>(word[s.len]) != b) return false;
         if (s.len + 1u == wlen) value_done(s);
         else s.len++;
