@@ -267,6 +267,43 @@ int tsm_json_is_complete(const tsm_json_state* s);
 int tsm_json_mask(void* stream, const tsm_vocab* vocab, const tsm_json_state* states, uint32_t rows,
                   uint32_t usable, uint32_t* mask, uint32_t mask_stride, char* err, size_t errlen);
 
+/* ---- the logits producer ------------------------------------------------
+ * Tachyon's output layer for the rows that get logits: xb = rmsnorm(x[r])
+ * in f32 (src/model.rs:702-709 over src/kernels.rs:522-528), then
+ * logits[r][v] = dot(W[v], xb) over a bf16 lm_head matrix W [vocab, dim]
+ * (src/model.rs:711-715, the Bf16 arm of src/weights.rs:230-239,
+ * src/kernels.rs:1411-1413), on the MFMA matrix cores.
+ * Replaces: the rmsnorm + lm_head.matmul pair of src/model.rs:700-716 (CPU)
+ * and src/gpu/mod.rs:1044-1047 (Metal), for a Bf16 lm_head.
+ *
+ * With TSM_LM_SPLIT each activation is carried as two bf16 values (hi =
+ * bf16(xb), lo = bf16(xb - hi), within 2^-17 of xb) and both are multiplied
+ * with W: twice the matrix work, activations about as exact as the
+ * reference's f32.  Without it the activations are rounded to bf16 once
+ * (relative error up to 2^-9 each).
+ */
+#define TSM_LM_SPLIT    1u
+#define TSM_LM_MAX_ROWS 65536u
+#define TSM_LM_MAX_DIM  32768u
+
+/* Device bytes tsm_lm_head needs as workspace for `rows` rows of `dim`
+ * (the bf16 operands, rows padded to 256). */
+size_t tsm_lm_head_workspace(uint32_t rows, uint32_t dim, uint32_t flags);
+
+/*
+ * Queues the logits of `rows` rows on `stream`: row r of x (f32, x + r *
+ * x_stride, dim values) is normalized with norm_w (f32 [dim]) and eps, and
+ * logits + r * ld receives its dot product with each of the vocab rows of w
+ * (bf16 [vocab][dim], 16-byte aligned).  dim is a multiple of 64 (at most
+ * TSM_LM_MAX_DIM); workspace (16-byte aligned, at least
+ * tsm_lm_head_workspace bytes) is overwritten.  All pointers are device
+ * pointers.  Allocates nothing; returns nonzero with a message on a bad
+ * argument, before anything is queued.
+ */
+int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* norm_w, float eps,
+                const uint16_t* w, uint32_t rows, uint32_t dim, uint32_t vocab, uint32_t flags, void* workspace,
+                size_t workspace_bytes, float* logits, uint32_t ld, char* err, size_t errlen);
+
 /* Library version string, e.g. "tachyon-sampler 0.1 gfx950". */
 const char* tsm_version(void);
 

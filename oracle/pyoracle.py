@@ -138,6 +138,11 @@ def lib():
                                     ctypes.POINTER(ctypes.c_int)]
         L.or_json_mask.restype = None
         L.or_json_mask.argtypes = [vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp]
+        L.or_rmsnorm.restype = None
+        L.or_rmsnorm.argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_float, vp]
+        L.or_matmul_bf16.restype = None
+        L.or_matmul_bf16.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32, vp,
+                                     ctypes.c_uint32]
         _lib = L
     return _lib
 
@@ -370,3 +375,29 @@ def json_check(text: bytes):
     ok, done = ctypes.c_int(), ctypes.c_int()
     lib().or_json_check(text, len(text), ctypes.byref(ok), ctypes.byref(done))
     return bool(ok.value), bool(done.value)
+
+
+def rmsnorm(x, w, eps):
+    """kernels.rs:522-528 per row of x (f32 [t, dim]): the reference's f32 arithmetic."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    for i in range(x.shape[0]):
+        lib().or_rmsnorm(_vp(x[i]), _vp(w), x.shape[1], float(eps), _vp(out[i]))
+    return out
+
+
+def matmul_bf16(w_bits, x):
+    """The Bf16 matmul (weights.rs:230-239): out[i][r] = dot_bf16(W[r], x[i]),
+    W as bf16 bit patterns (u16 [rows, dim]), x f32 [t, dim]."""
+    w_bits = np.ascontiguousarray(w_bits, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    rows, dim = w_bits.shape
+    out = np.empty((x.shape[0], rows), np.float32)
+    lib().or_matmul_bf16(_vp(w_bits), rows, dim, _vp(x), x.shape[0], _vp(out), rows)
+    return out
+
+
+def lm_head(x, norm_w, eps, w_bits):
+    """The output layer of model.rs:700-716 for a Bf16 lm_head: rmsnorm, then the matmul."""
+    return matmul_bf16(w_bits, rmsnorm(x, norm_w, eps))

@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 ROOT = os.path.dirname(HERE)
-SOURCES = ["tsm_sample.hip", "tsm_split.hip", "tsm_api.hip", "tsm_mask.hip"]
+SOURCES = ["tsm_sample.hip", "tsm_split.hip", "tsm_api.hip", "tsm_mask.hip", "tsm_lmhead.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 DEVICE_FLAGS = [

@@ -98,3 +98,23 @@ def test_argument_errors_need_no_device():
     st = _lib.TsmJsonState()
     assert L.tsm_json_mask(None, ctypes.byref(v), ctypes.byref(st), 1, 100, ctypes.byref(st), 1, err, len(err)) != 0
     assert b"mask_stride" in err.value
+
+
+def test_lm_head_arguments_are_checked_on_the_host():
+    L = _lib.lib()
+    err = ctypes.create_string_buffer(256)
+    # workspace: the bf16 operands of the rows padded to 256, twice when split
+    assert L.tsm_lm_head_workspace(1, 4096, 0) == 256 * 4096 * 2
+    assert L.tsm_lm_head_workspace(257, 4096, _lib.LM_SPLIT) == 512 * 4096 * 2 * 2
+    fake = ctypes.c_void_p(0x10000)  # never dereferenced: every case below fails its checks first
+    def call(rows=4, dim=128, vocab=100, flags=0, ws=1 << 20, ld=100, x_stride=128, w=fake):
+        return L.tsm_lm_head(None, fake, x_stride, fake, 1e-5, w, rows, dim, vocab, flags, fake, ws, fake, ld,
+                             err, len(err))
+    assert call(dim=100) != 0 and b"multiple of 64" in err.value
+    assert call(rows=0) != 0 and b"rows" in err.value
+    assert call(vocab=0) != 0 and b"vocab" in err.value
+    assert call(ld=99) != 0 and b"ld" in err.value
+    assert call(x_stride=64) != 0 and b"x_stride" in err.value
+    assert call(flags=4) != 0 and b"flags" in err.value
+    assert call(ws=1000) != 0 and b"workspace" in err.value
+    assert call(w=ctypes.c_void_p(0x10008)) != 0 and b"aligned" in err.value

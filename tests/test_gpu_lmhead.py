@@ -1,0 +1,147 @@
+"""GPU: the logits producer (tsm_lm_head) against the oracle's output layer
+(rmsnorm, kernels.rs:522-528, then the Bf16 matmul, weights.rs:230-239).
+
+Bar (floating point; the reference's own dot products fold in a
+platform-dependent order, so no bit pattern is the target):
+  * with TSM_LM_SPLIT every logit within 2^-16 * S of the oracle's, where
+    S = sum_k |W[v][k] * xb[r][k]| (f64) bounds the size of any rounding
+    of the sum; without it (activations rounded to bf16, relative error up
+    to 2^-9 each) within 2^-8 * S;
+  * on one-hot weights (a logit is then one activation) within 2^-16 (split)
+    or 2^-8 (bf16) of that activation: this pins the MFMA tile layout, the
+    vocabulary and row tails, the row stride and the output stride;
+  * split error at least 16 times below the bf16 mode's on the same inputs;
+  * columns past `vocab` in a wider output row are never written, and two
+    calls give identical logits.
+A wrong row, column or k index moves a logit by about the size of a whole
+dot product, far outside these bounds.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL_SPLIT = 2.0 ** -16
+TOL_BF16 = 2.0 ** -8
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def bf16_bits(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_f64(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def run(x, g, eps, wbits, split, ld=None, x_stride=None):
+    """tsm_lm_head through the Python wrapper; x f32 [rows, dim] (host), wbits u16 [vocab, dim]."""
+    import torch
+
+    from tachyon_amd.lmhead import lm_head
+
+    rows, dim = x.shape
+    vocab = wbits.shape[0]
+    xs = x_stride or dim
+    xd = torch.zeros(rows, xs, dtype=torch.float32, device="cuda")
+    xd[:, :dim] = torch.from_numpy(x).cuda()
+    xv = xd[:, :dim]
+    gd = torch.from_numpy(np.ascontiguousarray(g, np.float32)).cuda()
+    wd = torch.from_numpy(wbits.view(np.int16)).cuda().view(torch.bfloat16)
+    out = torch.full((rows, ld or vocab), -7.0, dtype=torch.float32, device="cuda")
+    lm_head(xv, gd, eps, wd, split=split, out=out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def bound_s(wbits, xb):
+    return np.abs(xb.astype(np.float64)) @ np.abs(bf16_f64(wbits)).T
+
+
+def check(case, got, want, s, tol):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    worst = float((err / np.maximum(s, 1e-30)).max())
+    say(f"{case}: max |gpu - oracle| / S = {worst:.3g} (bound {tol:.3g}), max abs {float(err.max()):.3g}")
+    assert np.all(err <= tol * s + 1e-30), case
+
+
+def test_one_hot_weights_pin_the_layout(oracle):
+    """Row v of W picks activation (5v + 3) mod dim: logit (r, v) is then
+    xb[r][(5v + 3) mod dim].  Rows 70 (not a multiple of 16 or 64), vocab 333
+    (not a multiple of 128), a row stride of dim + 8 and an output row of
+    vocab + 5 columns."""
+    rows, dim, vocab = 70, 128, 333
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 1.5, (rows, dim)).astype(np.float32)
+    g = rng.normal(1, 0.2, dim).astype(np.float32)
+    w = np.zeros((vocab, dim), np.float32)
+    pick = (5 * np.arange(vocab) + 3) % dim
+    w[np.arange(vocab), pick] = 1.0
+    wb = bf16_bits(w)
+    xb = oracle.rmsnorm(x, g, 1e-6)
+    want = xb[:, pick]
+    for split, tol in ((True, TOL_SPLIT), (False, TOL_BF16)):
+        say(f"one-hot rows={rows} dim={dim} vocab={vocab} split={split}")
+        got = run(x, g, 1e-6, wb, split, ld=vocab + 5, x_stride=dim + 8)
+        assert np.all(got[:, vocab:] == -7.0), "a column past vocab was written"
+        err = np.abs(got[:, :vocab].astype(np.float64) - want)
+        assert np.all(err <= tol * np.abs(want) + 1e-30), (split, float(err.max()))
+
+
+@pytest.mark.parametrize("rows,dim,vocab", [(1, 64, 1), (7, 128, 1000), (64, 640, 4099), (300, 256, 2000)])
+def test_random_against_the_oracle(oracle, rows, dim, vocab):
+    rng = np.random.default_rng(rows * 7919 + dim + vocab)
+    x = rng.normal(0, 2.0, (rows, dim)).astype(np.float32)
+    g = rng.normal(1, 0.3, dim).astype(np.float32)
+    wb = bf16_bits(rng.normal(0, 0.05, (vocab, dim)).astype(np.float32))
+    want = oracle.lm_head(x, g, 1e-5, wb)
+    xb = oracle.rmsnorm(x, g, 1e-5)
+    s = bound_s(wb, xb)
+    exact = xb.astype(np.float64) @ bf16_f64(wb).T
+    errs = {}
+    for split, tol in ((True, TOL_SPLIT), (False, TOL_BF16)):
+        case = f"random rows={rows} dim={dim} vocab={vocab} split={split}"
+        say(case)
+        got = run(x, g, 1e-5, wb, split)
+        check(case, got, want, s, tol)
+        errs[split] = float(np.sqrt(np.mean((got.astype(np.float64) - exact) ** 2)))
+    say(f"rms error vs exact: split {errs[True]:.3g}, bf16 {errs[False]:.3g}")
+    assert errs[True] * 16 <= errs[False]
+
+
+def test_full_size_sample(oracle):
+    """The bench shape: 256 rows, dim 4096, vocab 151936, checked on a sample
+    of 4 rows x 640 vocab ids (among them the last 128, the vocabulary's
+    partial tile), and twice in a row for identical results."""
+    import torch
+
+    from tachyon_amd.lmhead import lm_head
+
+    rows, dim, vocab = 256, 4096, 151936
+    say(f"full size rows={rows} dim={dim} vocab={vocab}")
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn(rows, dim, generator=gen, device="cuda", dtype=torch.float32) * 3.0
+    g = 1.0 + 0.2 * torch.randn(dim, generator=gen, device="cuda", dtype=torch.float32)
+    w = (torch.randn(vocab, dim, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    for split, tol in ((True, TOL_SPLIT), (False, TOL_BF16)):
+        out = lm_head(x, g, 1e-6, w, split=split)
+        out2 = lm_head(x, g, 1e-6, w, split=split)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2), "two calls differ"
+        rsel = np.array([0, 97, 200, 255])
+        rng = np.random.default_rng(8)
+        vsel = np.concatenate([rng.choice(vocab - 128, 512, replace=False), np.arange(vocab - 128, vocab)])
+        wb = w[torch.from_numpy(vsel).cuda()].view(torch.int16).cpu().numpy().view(np.uint16)
+        xs = x[torch.from_numpy(rsel).cuda()].cpu().numpy()
+        gs = g.cpu().numpy()
+        want = oracle.lm_head(xs, gs, 1e-6, wb)
+        s = bound_s(wb, oracle.rmsnorm(xs, gs, 1e-6))
+        got = out[torch.from_numpy(rsel).cuda()][:, torch.from_numpy(vsel).cuda()].cpu().numpy()
+        check(f"full size sample split={split}", got, want, s, tol)

@@ -517,3 +517,58 @@ def test_json_limits_hand_derived(oracle):
     assert not oracle.json_check(b'{"a": 1.}')[0]
     # after the object closes nothing follows, not even whitespace
     assert not oracle.json_check(b"{} ")[0]
+
+
+# ---- the output layer (oracle/lmhead_oracle.cpp) ---------------------------------
+
+def _bf16_bits(a):
+    """float32 -> bf16 bit patterns, round to nearest even (no NaNs here)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _bf16_f64(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_rmsnorm_closed_forms(oracle):
+    """kernels.rs:522-528: the mean (not the sum) of squares, eps inside the
+    square root, then x * inv * g.  A constant row of 0.5 with eps 0 has
+    inv exactly 2 and gives g back; with eps = 1 on a row of 3s inv is
+    1/sqrt(10); random rows agree with an f64 restatement to f32 rounding."""
+    g = np.linspace(-2.0, 3.0, 64).astype(np.float32)
+    out = oracle.rmsnorm(np.full((1, 64), 0.5, np.float32), g, 0.0)
+    assert np.array_equal(out[0], g)
+    out = oracle.rmsnorm(np.full((1, 64), 3.0, np.float32), np.ones(64, np.float32), 1.0)
+    assert np.allclose(out[0], 3.0 / math.sqrt(10.0), rtol=2e-7, atol=0)
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 2.0, (7, 96)).astype(np.float32)
+    w = rng.normal(1.0, 0.3, 96).astype(np.float32)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5) * w.astype(np.float64)
+    assert np.allclose(oracle.rmsnorm(x, w, 1e-5), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_matmul_bf16_selects_and_sums_exactly(oracle):
+    """weights.rs:230-239 / kernels.rs:1411-1413: out[i][r] = sum_k W[r][k] *
+    x[i][k].  One-hot rows of W (row r picks column (3r + 1) mod dim) on
+    non-square shapes pin the indexing and the operand order; small integers
+    give sums that f32 holds exactly, which must equal numpy's integer
+    product."""
+    rows, dim, t = 37, 64, 5
+    w = np.zeros((rows, dim), np.float32)
+    pick = (3 * np.arange(rows) + 1) % dim
+    w[np.arange(rows), pick] = 1.0
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, (t, dim)).astype(np.float32)
+    out = oracle.matmul_bf16(_bf16_bits(w), x)
+    assert out.shape == (t, rows)
+    assert np.array_equal(out, x[:, pick])
+    wi = rng.integers(-3, 4, (rows, dim))
+    xi = rng.integers(-5, 6, (t, dim))
+    out = oracle.matmul_bf16(_bf16_bits(wi.astype(np.float32)), xi.astype(np.float32))
+    assert np.array_equal(out, (xi @ wi.T).astype(np.float32))
+    # bf16 rounding of W is the reference's (round to nearest even): 1 + 2^-8
+    # (a tie) rounds to 1, 1 + 3 * 2^-8 to 1 + 2^-6
+    assert _bf16_bits(np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8], np.float32)).tolist() == [0x3F80, 0x3F82]
+    assert np.array_equal(_bf16_f64(_bf16_bits(np.array([1.5, -2.25], np.float32))), [1.5, -2.25])
