@@ -114,6 +114,11 @@ def main():
     ap.add_argument("--json-mask", action="store_true",
                     help="time the mask producer (tsm_json_mask) instead: 256 JsonObject rows over a "
                          "151936-token synthetic vocabulary")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="time the logits producer (tsm_lm_head) instead: 256 rows, dim 4096, vocab 151936, "
+                         "bf16 weights")
+    ap.add_argument("--lm-bf16", action="store_true",
+                    help="with --lm-head: activations rounded to bf16 (default: the hi/lo split)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run N MiB device copies for counter calibration instead of the bench")
     args = ap.parse_args()
@@ -135,6 +140,9 @@ def main():
         log(f"[bench] copied {args.calib_copy_mb} MiB x5")
         return
 
+    if args.lm_head:
+        bench_lm_head(args)
+        return
     if args.json_mask:
         bench_json_mask(args)
         return
@@ -314,6 +322,72 @@ def bench_json_mask(args):
                         "unit": "GB/s", "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                         "algorithmic_bytes_per_step": alg, "kernel_avg_us": round(us, 2),
                         "kernel": "json_mask_kernel (one launch per step)"},
+           "cpu_baseline": None, "oracle_check": check}
+    print(json.dumps(rec), flush=True)
+
+
+def bench_lm_head(args):
+    """One step of the logits producer at the c4 shape: 256 logit rows, a
+    Qwen-class hidden size of 4096 and vocabulary of 151936, random bf16
+    weights and f32 activations; the logits are checked against the oracle's
+    output layer on a sample after the timed region (the bound of
+    tests/test_gpu_lmhead.py)."""
+    import torch
+
+    from tachyon_amd.lmhead import lm_head, workspace_bytes
+
+    rows, dim, V = 256, 4096, 151936
+    split = not args.lm_bf16
+    gen = torch.Generator(device="cuda").manual_seed(0x1A4E)
+    x = torch.randn(rows, dim, generator=gen, device="cuda", dtype=torch.float32) * 3.0
+    g = 1.0 + 0.2 * torch.randn(dim, generator=gen, device="cuda", dtype=torch.float32)
+    w = (torch.randn(V, dim, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    out = torch.empty(rows, V, dtype=torch.float32, device="cuda")
+    ws = torch.empty(workspace_bytes(rows, dim, split), dtype=torch.uint8, device="cuda")
+    for _ in range(args.warmup):
+        lm_head(x, g, 1e-6, w, split=split, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    ea = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    eb = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        ea[i].record()
+        lm_head(x, g, 1e-6, w, split=split, out=out, workspace=ws)
+        eb[i].record()
+    torch.cuda.synchronize()
+    us = sum(ea[i].elapsed_time(eb[i]) for i in range(args.steps)) / args.steps * 1e3
+    check = None
+    if not args.no_check:
+        import numpy as np
+
+        from oracle import pyoracle
+
+        rsel = np.array([0, 85, 170, 255])
+        vsel = np.concatenate([np.arange(0, V - 128, (V - 128) // 512)[:512], np.arange(V - 128, V)])
+        rt, vt = torch.from_numpy(rsel).cuda(), torch.from_numpy(vsel).cuda()
+        wb = w[vt].view(torch.int16).cpu().numpy().view(np.uint16)
+        xs, gs = x[rt].cpu().numpy(), g.cpu().numpy()
+        want = pyoracle.lm_head(xs, gs, 1e-6, wb)
+        xb = pyoracle.rmsnorm(xs, gs, 1e-6).astype(np.float64)
+        s_abs = np.abs(xb) @ np.abs((wb.astype(np.uint32) << 16).view(np.float32).astype(np.float64)).T
+        got = out[rt][:, vt].cpu().numpy().astype(np.float64)
+        tol = 2.0 ** -16 if split else 2.0 ** -8
+        check = {"rows": int(len(rsel)), "ids": int(len(vsel)),
+                 "within_bound": int((np.abs(got - want) <= tol * s_abs).sum()), "bound": f"{tol:.3g} * sum|w x|"}
+    alg = V * dim * 2 + rows * dim * 4 + dim * 4 + rows * V * 4
+    flop = 2.0 * rows * dim * V
+    rec = {"metric": "lm_head logit rows/s (rmsnorm + bf16 lm_head, dim 4096, vocab 151936)",
+           "value": round(rows / (us * 1e-6), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16 weights, " + ("bf16 hi+lo activations" if split else "bf16 activations"),
+           "data": "synthetic",
+           "config": {"workload": "tsm_lm_head: 256 rows x dim 4096 x vocab 151936 (the c4 batch's logits)",
+                      "rows": rows, "dim": dim, "vocab": V, "split": split},
+           "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                        "algorithmic_bytes_per_step": alg, "kernel_avg_us": round(us, 2),
+                        "kernel": "lm_prep_kernel + lm_gemm_kernel (one tsm_lm_head call per step)",
+                        "mfma_tflops": round(flop * (2 if split else 1) / (us * 1e-6) / 1e12, 1),
+                        "mfma_peak_tflops": 2500.0},
            "cpu_baseline": None, "oracle_check": check}
     print(json.dumps(rec), flush=True)
 

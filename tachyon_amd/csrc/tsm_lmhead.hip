@@ -9,25 +9,36 @@
 //                   as bf16 MFMA operands in the caller's workspace: hi =
 //                   bf16(xb), and with TSM_LM_SPLIT also lo = bf16(xb - hi),
 //                   so that hi + lo carries xb to within 2^-17 of itself and
-//                   the products with bf16 weights stay exact in f32.  Rows
+//                   the products with bf16 weights stay exact in f32.  The
+//                   operands are stored in MFMA fragment order (frag_pos), so
+//                   that a wave's fragment load is 1 KB in one piece; rows
 //                   past `rows` up to the tile are zero.
 //   lm_gemm_kernel  logits = A W^T on v_mfma_f32_16x16x32_bf16.  A workgroup
-//                   (4 waves) owns 256 rows x 128 vocab ids; wave w the rows
-//                   64w..64w+63 (4 x 8 MFMA tiles of 16 x 16, 128 f32
-//                   accumulators per lane).  The weight tile of each k-step
-//                   (128 ids x 64 k, 16 KB) is loaded cooperatively four
-//                   steps ahead into a register ring (4 x 16 B per thread
-//                   per step), written to one of two LDS buffers the step
+//                   (8 waves, two per SIMD) owns 256 rows x 128 vocab ids;
+//                   wave w the rows 32w..32w+31 (2 x 8 MFMA tiles of 16 x 16,
+//                   64 f32 accumulators per lane).  The weight tile of each
+//                   k-step (128 ids x 64 k, 16 KB) is loaded cooperatively
+//                   four steps ahead into a register ring (2 x 16 B per thread
+//                   per step), staged into one of three LDS buffers two steps
 //                   before it is used, and read back as MFMA fragments by
-//                   every wave; one barrier per step.  A's fragments (the
-//                   workspace, 2-4 MB, resident in L2) are loaded by each
-//                   wave straight into registers one step ahead.
+//                   every wave half a step ahead of its MFMAs; one barrier per
+//                   step.  A's fragments (the workspace, 2-4 MB, resident in
+//                   L2) are loaded by each wave straight into registers one
+//                   step ahead.
+//
+// Measured at 256 rows x dim 4096 x vocab 151,936 (MI355X): 466 us (bf16
+// activations) and 676 us (split), against 175 us for the bytes at 8 TB/s.
+// One wave per SIMD issues these MFMAs at about half the peak rate (a
+// microbenchmark of independent MFMAs: 52% with one wave, 76% with two),
+// hence the 8-wave workgroup; the loads of both operands, the LDS reads and
+// the barrier each add to the step time (variants with each switched off).
 //
 // Both operands are contiguous along k (A's rows, W's rows), so every MFMA
 // fragment (8 consecutive k of one row) is one 16-byte load.
 #include <cstdarg>
 #include <cstdio>
 #include <type_traits>
+#include <utility>
 
 #include <hip/hip_runtime.h>
 
@@ -40,15 +51,37 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 raw bytes
 
-constexpr uint32_t kThreads = 256;            // 4 waves
-constexpr uint32_t kTileM = 256;              // rows per workgroup (64 per wave)
-constexpr uint32_t kTileN = 128;              // vocab ids per workgroup
-constexpr uint32_t kStepK = 64;               // k per step: two MFMA k-halves of 32
-constexpr uint32_t kRing = 4;                 // weight steps in flight per thread
-constexpr uint32_t kRowB = kStepK * 2 + 16;   // LDS bytes per weight row (16 B pad: no bank conflicts)
-constexpr uint32_t kBufB = kTileN * kRowB;    // one LDS weight buffer (18,432 B)
+constexpr uint32_t kPrepThreads = 256;  // the prep kernel: 4 waves per row
+
+#ifndef TSM_LM_WAVES_M
+#define TSM_LM_WAVES_M 8
+#endif
+#ifndef TSM_LM_WAVES_N
+#define TSM_LM_WAVES_N 1
+#endif
+#ifndef TSM_LM_RING
+#define TSM_LM_RING 4
+#endif
+#ifndef TSM_LM_ASETS
+#define TSM_LM_ASETS 2
+#endif
+constexpr uint32_t kTileM = 256;                        // rows per workgroup
+constexpr uint32_t kWavesM = TSM_LM_WAVES_M;            // waves along the rows
+constexpr uint32_t kWavesN = TSM_LM_WAVES_N;            // waves along the vocabulary
+constexpr uint32_t kThreads = 64 * kWavesM * kWavesN;
+constexpr uint32_t kRowsW = kTileM / kWavesM;           // rows per wave
+constexpr uint32_t kMBlk = kRowsW / 16;                 // 16-row MFMA blocks per wave
+constexpr uint32_t kTileN = 128;                        // vocab ids per workgroup
+constexpr uint32_t kNBlk = kTileN / kWavesN / 16;       // 16-id MFMA blocks per wave
+constexpr uint32_t kStepK = 64;                         // k per step: two MFMA k-halves of 32
+constexpr uint32_t kRing = TSM_LM_RING;                 // weight steps in flight per thread
+constexpr uint32_t kASets = TSM_LM_ASETS;               // A steps held per wave (the one in use and those ahead)
+constexpr uint32_t kRowB = kStepK * 2 + 16;             // LDS bytes per weight row (16 B pad: no bank conflicts)
+constexpr uint32_t kBufB = kTileN * kRowB;              // one LDS weight buffer (18,432 B)
 constexpr uint32_t kChunks = kTileN * kStepK * 2 / 16 / kThreads;  // 16-byte weight chunks per thread per step
-static_assert(kChunks == 4, "weight tile split");
+static_assert(kChunks * kThreads * 16 == kTileN * kStepK * 2, "weight tile split");
+static_assert(kRing % kASets == 0, "A sets follow the ring slots");
+static_assert(kRing >= 3, "a step is staged two steps ahead");
 
 struct PrepArgs {
     const float* x;
@@ -75,36 +108,68 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
 }
 __device__ __forceinline__ float bf16_f32(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
+// The operands' layout in the workspace: MFMA fragment order.  The 16 x 32
+// block (rows 16 rb.., k 32 kc..) is 1 KB, lane l's 8 values (row 16 rb +
+// (l & 15), k 32 kc + 8 (l >> 4) ..) at bytes 16 l, and the blocks of one
+// row block follow each other along k; so a wave's fragment load reads 1 KB
+// in one piece.  frag_pos is the element offset of (row, k), k a multiple of 8.
+__device__ __forceinline__ size_t frag_pos(uint32_t row, uint32_t k, uint32_t dim) {
+    const uint32_t lane = (row & 15u) + 16u * ((k >> 3) & 3u);
+    return ((static_cast<size_t>(row >> 4) * (dim >> 5) + (k >> 5)) * 64u + lane) * 8u;
+}
+
 // One workgroup per (padded) row: the rmsnorm of kernels.rs:522-528,
 // ss = (sum of x^2) / dim, inv = 1 / sqrt(ss + eps), out = x * inv * g, all
 // in f32 (the sum in tree order rather than the reference's left fold).
-__global__ __launch_bounds__(kThreads) void lm_prep_kernel(PrepArgs a) {
-    __shared__ float part[kThreads / 64];
+__global__ __launch_bounds__(kPrepThreads) void lm_prep_kernel(PrepArgs a) {
+    __shared__ float part[kPrepThreads / 64];
+    static_assert(kPrepThreads == 256, "the reduction below sums four wave partials");
     const uint32_t r = blockIdx.x, tid = threadIdx.x;
-    uint16_t* hi = a.ahi + static_cast<size_t>(r) * a.dim;
-    uint16_t* lo = a.alo ? a.alo + static_cast<size_t>(r) * a.dim : nullptr;
+    const uint32_t nchunk = a.dim / 8u;  // 8 consecutive k per chunk: one lane's fragment
     if (r >= a.rows) {  // padding rows of the last tile
-        for (uint32_t k = tid; k < a.dim; k += kThreads) {
-            hi[k] = 0;
-            if (lo) lo[k] = 0;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        for (uint32_t c = tid; c < nchunk; c += kPrepThreads) {
+            *reinterpret_cast<u32x4*>(a.ahi + frag_pos(r, 8u * c, a.dim)) = z;
+            if (a.alo) *reinterpret_cast<u32x4*>(a.alo + frag_pos(r, 8u * c, a.dim)) = z;
         }
         return;
     }
     const float* x = a.x + static_cast<size_t>(r) * a.x_stride;
     float s = 0.0f;
-    for (uint32_t k = tid; k < a.dim; k += kThreads) s += x[k] * x[k];
+    for (uint32_t k = tid; k < a.dim; k += kPrepThreads) s += x[k] * x[k];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
     if ((tid & 63u) == 0) part[tid >> 6] = s;
     __syncthreads();
     const float ss = ((part[0] + part[1]) + (part[2] + part[3])) / static_cast<float>(a.dim);
     const float inv = 1.0f / sqrtf(ss + a.eps);
-    for (uint32_t k = tid; k < a.dim; k += kThreads) {
-        const float o = x[k] * inv * a.norm_w[k];
-        const uint16_t h = bf16_rne(o);
-        hi[k] = h;
-        if (lo) lo[k] = bf16_rne(o - bf16_f32(h));
+    for (uint32_t c = tid; c < nchunk; c += kPrepThreads) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (uint32_t e = 0; e < 8; e += 2) {
+            const uint32_t k = 8u * c + e;
+            const float o0 = x[k] * inv * a.norm_w[k];
+            const float o1 = x[k + 1u] * inv * a.norm_w[k + 1u];
+            const uint16_t h0 = bf16_rne(o0), h1 = bf16_rne(o1);
+            hw[e / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+            lw[e / 2] = static_cast<uint32_t>(bf16_rne(o0 - bf16_f32(h0))) |
+                        (static_cast<uint32_t>(bf16_rne(o1 - bf16_f32(h1))) << 16);
+        }
+        const size_t pos = frag_pos(r, 8u * c, a.dim);
+        *reinterpret_cast<u32x4*>(a.ahi + pos) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        if (a.alo) *reinterpret_cast<u32x4*>(a.alo + pos) = u32x4{lw[0], lw[1], lw[2], lw[3]};
     }
+}
+
+// Calls f(std::integral_constant<uint32_t, Q>) for Q = 0 .. N-1 in order:
+// register arrays indexed by Q are then indexed by constants.
+template <uint32_t N, class F, uint32_t... Q>
+__device__ __forceinline__ void each_slot_(F&& f, std::integer_sequence<uint32_t, Q...>) {
+    (f(std::integral_constant<uint32_t, Q>{}), ...);
+}
+template <uint32_t N, class F>
+__device__ __forceinline__ void each_slot(F&& f) {
+    each_slot_<N>(f, std::make_integer_sequence<uint32_t, N>{});
 }
 
 __device__ __forceinline__ bf16x8 frag(const uint16_t* p) {
@@ -117,28 +182,29 @@ __device__ __forceinline__ bf16x8 frag(const uint16_t* p) {
 // not stored.
 template <bool kSplit>
 __global__ __launch_bounds__(kThreads) void lm_gemm_kernel(GemmArgs a) {
-    __shared__ __align__(16) uint8_t lds[2 * kBufB];
+    __shared__ __align__(16) uint8_t lds[3 * kBufB];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t n0 = blockIdx.x * kTileN;
-    const uint32_t m0 = blockIdx.y * kTileM + wave * 64u;
+    const uint32_t wn0 = (wave / kWavesM) * (kTileN / kWavesN);  // this wave's first id in the tile
+    const uint32_t m0 = blockIdx.y * kTileM + (wave % kWavesM) * kRowsW;
     const uint32_t dim = a.dim, nsteps = dim / kStepK;
 
-    // this thread's weight chunks: rows (tid >> 3) + 32 i, k offset 8 * (tid & 7)
+    // this thread's weight chunks: rows (tid >> 3) + (kThreads / 8) i, k offset 8 * (tid & 7)
     const uint16_t* wp[kChunks];
     uint32_t woff[kChunks];
 #pragma unroll
     for (uint32_t i = 0; i < kChunks; i++) {
-        const uint32_t row = (tid >> 3) + 32u * i;
+        const uint32_t row = (tid >> 3) + (kThreads / 8u) * i;
         const uint32_t v = min(n0 + row, a.vocab - 1u);
         wp[i] = a.w + static_cast<size_t>(v) * dim + 8u * (tid & 7u);
         woff[i] = row * kRowB + 16u * (tid & 7u);
     }
     // this lane's A fragments: rows m0 + 16 i + (lane & 15), k offset 8 * (lane >> 4)
-    const size_t aoff = static_cast<size_t>(m0 + (lane & 15u)) * dim + 8u * (lane >> 4);
+    const size_t aoff = static_cast<size_t>(m0 >> 4) * (dim >> 5) * 512u + 8u * lane;
     const uint16_t* ah = a.ahi + aoff;
     const uint16_t* al = kSplit ? a.alo + aoff : nullptr;
     // this lane's weight fragments in LDS: row 16 j + (lane & 15), bytes 16 * (lane >> 4)
-    const uint32_t foff = (lane & 15u) * kRowB + 16u * (lane >> 4);
+    const uint32_t foff = (wn0 + (lane & 15u)) * kRowB + 16u * (lane >> 4);
 
     u32x4 ring[kRing][kChunks];
     auto issue = [&](uint32_t s, u32x4 (&dst)[kChunks]) __attribute__((always_inline)) {
@@ -150,89 +216,102 @@ __global__ __launch_bounds__(kThreads) void lm_gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (uint32_t i = 0; i < kChunks; i++) *reinterpret_cast<u32x4*>(lds + buf * kBufB + woff[i]) = src[i];
     };
-    bf16x8 ahf[2][4][2], alf[2][4][2];
+    bf16x8 ahf[kASets][kMBlk][2], alf[kASets][kMBlk][2];
     auto load_a = [&](uint32_t s, uint32_t set) __attribute__((always_inline)) {
         const uint32_t k0 = s * kStepK;
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++)
+        for (uint32_t i = 0; i < kMBlk; i++)
 #pragma unroll
             for (uint32_t h = 0; h < 2; h++) {
-                const size_t o = static_cast<size_t>(16u * i) * dim + k0 + 32u * h;
+                const size_t o = (static_cast<size_t>(i) * (dim >> 5) + (k0 >> 5) + h) * 512u;
                 ahf[set][i][h] = frag(ah + o);
                 if (kSplit) alf[set][i][h] = frag(al + o);
             }
     };
 
-    f32x4 acc[4][8];
+    f32x4 acc[kMBlk][kNBlk];
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++)
+    for (uint32_t i = 0; i < kMBlk; i++)
 #pragma unroll
-        for (uint32_t j = 0; j < 8; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t j = 0; j < kNBlk; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // One k-step s = s0 + Q (Q a compile-time ring slot, so that every
     // register array is indexed by constants): stage step s + 1, fetch A of
     // step s + 1, put step s + kRing in flight, then the MFMAs of step s.
-    // The loads and stores are unconditional (a step past the last one reads
-    // the last one again, into a buffer no step reads), so that no two paths
-    // meet with different ring slots: the ring then stays in registers.
+    // Half-step h of step t: the weight fragments (k 32 h .. 32 h + 31 of
+    // the tile's 64) from LDS buffer t % 3.
+    auto read_w = [&](bf16x8 (&wf)[kNBlk], uint32_t t, uint32_t h) __attribute__((always_inline)) {
+        const uint8_t* wb = lds + (t % 3u) * kBufB + foff + 64u * h;
+#pragma unroll
+        for (uint32_t j = 0; j < kNBlk; j++) wf[j] = *reinterpret_cast<const bf16x8*>(wb + j * 16u * kRowB);
+    };
+    auto mfmas = [&](const bf16x8 (&wf)[kNBlk], const bf16x8 (&a)[kMBlk][2], uint32_t h) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t i = 0; i < kMBlk; i++)
+#pragma unroll
+            for (uint32_t j = 0; j < kNBlk; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i][h], wf[j], acc[i][j], 0, 0, 0);
+    };
+    bf16x8 wc[kNBlk], wn[kNBlk];  // this half-step's weight fragments and the next one's
+
+    // Step s = s0 + Q (Q a compile-time ring slot, so that every register
+    // array is indexed by constants).  Three LDS buffers: step t is staged
+    // into buffer t % 3 at step t - 2 and read at steps t - 1 (its first
+    // half) and t (its second), so each half-step's LDS reads overlap the
+    // MFMAs of the one before.  The loads and stores are unconditional (a
+    // step past the last one reads the last one again, into a buffer no
+    // MFMA uses), so that no two paths meet with different ring slots: the
+    // ring then stays in registers.
     auto body = [&](uint32_t s0, auto qc) __attribute__((always_inline)) {
         constexpr uint32_t Q = decltype(qc)::value;
         const uint32_t s = s0 + Q;
-        // every wave is done with buffer (s + 1) & 1 (step s - 1) and sees
-        // step s in buffer s & 1
+        // every wave is done with buffer (s + 2) % 3 (step s - 1) and sees
+        // step s + 1 in buffer (s + 1) % 3
         __syncthreads();
-        stage(ring[(Q + 1u) % kRing], (s + 1u) & 1u);
-        load_a(min(s + 1u, nsteps - 1u), (Q + 1u) & 1u);
+        stage(ring[(Q + 2u) % kRing], (s + 2u) % 3u);
+        load_a(min(s + kASets - 1u, nsteps - 1u), (Q + kASets - 1u) % kASets);
         issue(min(s + kRing, nsteps - 1u), ring[Q]);
-        if (s >= nsteps) return;
-        const uint8_t* wb = lds + (s & 1u) * kBufB + foff;
-#pragma unroll
-        for (uint32_t h = 0; h < 2; h++) {
-            bf16x8 wf[8];
-#pragma unroll
-            for (uint32_t j = 0; j < 8; j++)
-                wf[j] = *reinterpret_cast<const bf16x8*>(wb + j * 16u * kRowB + 64u * h);
-#pragma unroll
-            for (uint32_t i = 0; i < 4; i++)
-#pragma unroll
-                for (uint32_t j = 0; j < 8; j++) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahf[Q & 1u][i][h], wf[j], acc[i][j], 0, 0, 0);
-                    if (kSplit)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alf[Q & 1u][i][h], wf[j], acc[i][j], 0, 0, 0);
-                }
+        read_w(wn, s, 1);
+        const bool live = s < nsteps;
+        if (live) {
+            mfmas(wc, ahf[Q % kASets], 0);
+            if (kSplit) mfmas(wc, alf[Q % kASets], 0);
+        }
+        read_w(wc, s + 1u, 0);
+        if (live) {
+            mfmas(wn, ahf[Q % kASets], 1);
+            if (kSplit) mfmas(wn, alf[Q % kASets], 1);
         }
     };
-    using C0 = std::integral_constant<uint32_t, 0>;
-    using C1 = std::integral_constant<uint32_t, 1>;
-    using C2 = std::integral_constant<uint32_t, 2>;
-    using C3 = std::integral_constant<uint32_t, 3>;
-    static_assert(kRing == 4, "the ring slots below");
 
-    // prologue: steps 0 .. kRing - 1 in flight, step 0 staged, A of step 0 loaded
-    issue(0, ring[0]);
-    issue(min(1u, nsteps - 1u), ring[1]);
-    issue(min(2u, nsteps - 1u), ring[2]);
-    issue(min(3u, nsteps - 1u), ring[3]);
+    // prologue: steps 0 .. kRing - 1 in flight, steps 0 and 1 staged, A of
+    // the first kASets - 1 steps loaded, the first half of step 0 read
+    each_slot<kRing>([&](auto qc) __attribute__((always_inline)) {
+        constexpr uint32_t Q = decltype(qc)::value;
+        issue(min(Q, nsteps - 1u), ring[Q]);
+    });
     stage(ring[0], 0);
-    load_a(0, 0);
-    for (uint32_t s0 = 0; s0 < nsteps; s0 += kRing) {
-        body(s0, C0{});
-        body(s0, C1{});
-        body(s0, C2{});
-        body(s0, C3{});
-    }
+    stage(ring[1], 1);
+    each_slot<kASets - 1>([&](auto qc) __attribute__((always_inline)) {
+        constexpr uint32_t Q = decltype(qc)::value;
+        load_a(min(Q, nsteps - 1u), Q);
+    });
+    __syncthreads();
+    read_w(wc, 0, 0);
+    for (uint32_t s0 = 0; s0 < nsteps; s0 += kRing)
+        each_slot<kRing>([&](auto qc) __attribute__((always_inline)) { body(s0, qc); });
 
     // lane l holds rows 4 (l >> 4) + e, column l & 15 of each 16 x 16 tile
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++)
+    for (uint32_t i = 0; i < kMBlk; i++)
 #pragma unroll
         for (uint32_t e = 0; e < 4; e++) {
             const uint32_t row = m0 + 16u * i + 4u * (lane >> 4) + e;
             if (row >= a.rows) continue;
             float* out = a.logits + static_cast<size_t>(row) * a.ld;
 #pragma unroll
-            for (uint32_t j = 0; j < 8; j++) {
-                const uint32_t col = n0 + 16u * j + (lane & 15u);
+            for (uint32_t j = 0; j < kNBlk; j++) {
+                const uint32_t col = n0 + wn0 + 16u * j + (lane & 15u);
                 if (col < a.vocab) out[col] = acc[i][j][e];
             }
         }
@@ -295,7 +374,7 @@ int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* no
     p.rows_pad = rp;
     p.dim = dim;
     p.x_stride = x_stride;
-    hipLaunchKernelGGL(tsm::lm::lm_prep_kernel, dim3(rp), dim3(tsm::lm::kThreads), 0, st, p);
+    hipLaunchKernelGGL(tsm::lm::lm_prep_kernel, dim3(rp), dim3(tsm::lm::kPrepThreads), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "prep launch failed: %s", hipGetErrorString(e)), 1;
 
