@@ -145,3 +145,44 @@ def test_full_size_sample(oracle):
         s = bound_s(wb, oracle.rmsnorm(xs, gs, 1e-6))
         got = out[torch.from_numpy(rsel).cuda()][:, torch.from_numpy(vsel).cuda()].cpu().numpy()
         check(f"full size sample split={split}", got, want, s, tol)
+
+
+def test_logits_feed_the_sampler(oracle):
+    """The producer's logits stay on the device and go straight into
+    tsm_sample (row stride = vocab): rows with the c4 settings (repetition,
+    presence and frequency penalties over a history, top-k, top-p, min-p,
+    top-5 logprobs) and plain temperature rows sampled from them equal the
+    oracle's sampling of the same logits, copied back, in every token, kept
+    count and probability (the sampler's own bar)."""
+    import dataclasses
+
+    import torch
+
+    from parity import check
+    from tachyon_amd import workloads as wl
+    from tachyon_amd.device import Outputs, SamplerContext, upload
+    from tachyon_amd.lmhead import lm_head
+
+    rows, dim, vocab = 48, 512, 32000
+    say(f"lm_head -> tsm_sample rows={rows} dim={dim} vocab={vocab}")
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    x = torch.randn(rows, dim, generator=gen, device="cuda", dtype=torch.float32) * 3.0
+    g = 1.0 + 0.2 * torch.randn(dim, generator=gen, device="cuda", dtype=torch.float32)
+    w = (torch.randn(vocab, dim, generator=gen, device="cuda", dtype=torch.float32) * 0.1).to(torch.bfloat16)
+    logits = lm_head(x, g, 1e-6, w, split=True)
+    rng = np.random.default_rng(32)
+    params = wl.make_params(rows, temperature=0.7, top_k=64, top_p=0.92, repetition_penalty=1.1,
+                            presence_penalty=0.4, frequency_penalty=0.2, min_p=0.02, flags=2, n_logprobs=5)
+    params[rows // 2:] = wl.make_params(rows - rows // 2, temperature=1.0, top_p=0.95)
+    hist = [rng.integers(0, vocab, 128).astype(np.uint32) for _ in range(rows)]
+    offs = np.zeros(rows + 1, np.uint32)
+    offs[1:] = np.cumsum([len(h) for h in hist])
+    host = wl.Workload("lm->sample", logits.cpu().numpy(), vocab, params, np.concatenate(hist), offs, None,
+                       wl.uniforms(rng, rows), top_stride=5)
+    b = dataclasses.replace(upload(host), logits=logits)  # the producer's own buffer
+    ctx = SamplerContext(rows, vocab)
+    out = Outputs(rows, 5)
+    ctx.sample(b, out)
+    torch.cuda.synchronize()
+    assert ctx.status() == 0
+    check(host, out.numpy(), oracle.sample_batch(host), "lm_head -> tsm_sample")
