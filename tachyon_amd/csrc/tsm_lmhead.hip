@@ -52,6 +52,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 raw bytes
 
 constexpr uint32_t kPrepThreads = 256;  // the prep kernel: 4 waves per row
+constexpr uint32_t kPrepChunks = 16;    // 8-value chunks per prep thread: dim up to 32768
 
 #ifndef TSM_LM_WAVES_M
 #define TSM_LM_WAVES_M 8
@@ -124,6 +125,7 @@ __device__ __forceinline__ size_t frag_pos(uint32_t row, uint32_t k, uint32_t di
 __global__ __launch_bounds__(kPrepThreads) void lm_prep_kernel(PrepArgs a) {
     __shared__ float part[kPrepThreads / 64];
     static_assert(kPrepThreads == 256, "the reduction below sums four wave partials");
+    static_assert(kPrepThreads * kPrepChunks * 8 >= TSM_LM_MAX_DIM, "a row fits the threads' chunks");
     const uint32_t r = blockIdx.x, tid = threadIdx.x;
     const uint32_t nchunk = a.dim / 8u;  // 8 consecutive k per chunk: one lane's fragment
     if (r >= a.rows) {  // padding rows of the last tile
@@ -134,22 +136,44 @@ __global__ __launch_bounds__(kPrepThreads) void lm_prep_kernel(PrepArgs a) {
         }
         return;
     }
+    // the row is read once: each thread keeps its chunks (8 values each, at
+    // most kPrepChunks) in registers between the sum of squares and the
+    // normalization
     const float* x = a.x + static_cast<size_t>(r) * a.x_stride;
+    f32x4 v[kPrepChunks][2];
     float s = 0.0f;
-    for (uint32_t k = tid; k < a.dim; k += kPrepThreads) s += x[k] * x[k];
+#pragma unroll
+    for (uint32_t j = 0; j < kPrepChunks; j++) {
+        const uint32_t c = tid + j * kPrepThreads;
+        if (c < nchunk) {
+            // x rows are 16-byte aligned only when x_stride and the base are; read by element
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++) {
+                v[j][0][e] = x[8u * c + e];
+                v[j][1][e] = x[8u * c + 4u + e];
+            }
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++) s += v[j][0][e] * v[j][0][e];
+#pragma unroll
+            for (uint32_t e = 0; e < 4; e++) s += v[j][1][e] * v[j][1][e];
+        }
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
     if ((tid & 63u) == 0) part[tid >> 6] = s;
     __syncthreads();
     const float ss = ((part[0] + part[1]) + (part[2] + part[3])) / static_cast<float>(a.dim);
     const float inv = 1.0f / sqrtf(ss + a.eps);
-    for (uint32_t c = tid; c < nchunk; c += kPrepThreads) {
+#pragma unroll
+    for (uint32_t j = 0; j < kPrepChunks; j++) {
+        const uint32_t c = tid + j * kPrepThreads;
+        if (c >= nchunk) continue;
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (uint32_t e = 0; e < 8; e += 2) {
             const uint32_t k = 8u * c + e;
-            const float o0 = x[k] * inv * a.norm_w[k];
-            const float o1 = x[k + 1u] * inv * a.norm_w[k + 1u];
+            const float o0 = v[j][e >> 2][e & 3u] * inv * a.norm_w[k];
+            const float o1 = v[j][e >> 2][(e & 3u) + 1u] * inv * a.norm_w[k + 1u];
             const uint16_t h0 = bf16_rne(o0), h1 = bf16_rne(o1);
             hw[e / 2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
             lw[e / 2] = static_cast<uint32_t>(bf16_rne(o0 - bf16_f32(h0))) |

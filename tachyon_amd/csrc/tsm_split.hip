@@ -1624,16 +1624,15 @@ __global__ __launch_bounds__(kSB) void split_kernel(SplitArgs a) {
             E.pidf[r] = e.y;
         }
     }
-    // row statistics: the raw maximum, the bounds, allowed ids, flags, and
-    // the logsumexp (sampler.rs:298-304)
+    // row statistics: the raw maximum, the bounds, flags, and the
+    // logsumexp (sampler.rs:298-304)
     float xmax_row = -INFINITY, t_star = -INFINITY, tal_star = -INFINITY;
-    uint32_t nallow_row = 0, flags_row = 0;
+    uint32_t flags_row = 0;
     for (uint32_t sg = tid; sg < nseg; sg += kSB) {
         const SegSum S = sg == tid ? mysum : ld_sum(sums + sg);
         xmax_row = fmaxf(xmax_row, S.xmax);
         t_star = fmaxf(t_star, S.tall);
         if (S.tal == S.tal) tal_star = fmaxf(tal_star, S.tal);
-        nallow_row += S.nallow;
         flags_row |= S.flags;
     }
     {
