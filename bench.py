@@ -117,6 +117,7 @@ def main():
     ap.add_argument("--lm-head", action="store_true",
                     help="time the logits producer (tsm_lm_head) instead: 256 rows, dim 4096, vocab 151936, "
                          "bf16 weights")
+    ap.add_argument("--lm-rows", type=int, default=256, help="with --lm-head: logit rows per call (256: the c4 batch)")
     ap.add_argument("--lm-bf16", action="store_true",
                     help="with --lm-head: activations rounded to bf16 (default: the hi/lo split)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
@@ -336,7 +337,7 @@ def bench_lm_head(args):
 
     from tachyon_amd.lmhead import lm_head, workspace_bytes
 
-    rows, dim, V = 256, 4096, 151936
+    rows, dim, V = args.lm_rows, 4096, 151936
     split = not args.lm_bf16
     gen = torch.Generator(device="cuda").manual_seed(0x1A4E)
     x = torch.randn(rows, dim, generator=gen, device="cuda", dtype=torch.float32) * 3.0
@@ -361,7 +362,7 @@ def bench_lm_head(args):
 
         from oracle import pyoracle
 
-        rsel = np.array([0, 85, 170, 255])
+        rsel = np.unique(np.array([0, rows // 3, (2 * rows) // 3, rows - 1]))
         vsel = np.concatenate([np.arange(0, V - 128, (V - 128) // 512)[:512], np.arange(V - 128, V)])
         rt, vt = torch.from_numpy(rsel).cuda(), torch.from_numpy(vsel).cuda()
         wb = w[vt].view(torch.int16).cpu().numpy().view(np.uint16)
@@ -380,7 +381,8 @@ def bench_lm_head(args):
            "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "bf16 weights, " + ("bf16 hi+lo activations" if split else "bf16 activations"),
            "data": "synthetic",
-           "config": {"workload": "tsm_lm_head: 256 rows x dim 4096 x vocab 151936 (the c4 batch's logits)",
+           "config": {"workload": f"tsm_lm_head: {rows} rows x dim 4096 x vocab 151936"
+                                  + (" (the c4 batch's logits)" if rows == 256 else ""),
                       "rows": rows, "dim": dim, "vocab": V, "split": split},
            "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,

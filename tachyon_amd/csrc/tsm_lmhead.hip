@@ -54,35 +54,35 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16 raw bytes
 constexpr uint32_t kPrepThreads = 256;  // the prep kernel: 4 waves per row
 constexpr uint32_t kPrepChunks = 16;    // 8-value chunks per prep thread: dim up to 32768
 
-#ifndef TSM_LM_WAVES_M
-#define TSM_LM_WAVES_M 8
-#endif
-#ifndef TSM_LM_WAVES_N
-#define TSM_LM_WAVES_N 1
-#endif
-#ifndef TSM_LM_RING
-#define TSM_LM_RING 4
-#endif
-#ifndef TSM_LM_ASETS
-#define TSM_LM_ASETS 2
-#endif
-constexpr uint32_t kTileM = 256;                        // rows per workgroup
-constexpr uint32_t kWavesM = TSM_LM_WAVES_M;            // waves along the rows
-constexpr uint32_t kWavesN = TSM_LM_WAVES_N;            // waves along the vocabulary
-constexpr uint32_t kThreads = 64 * kWavesM * kWavesN;
-constexpr uint32_t kRowsW = kTileM / kWavesM;           // rows per wave
-constexpr uint32_t kMBlk = kRowsW / 16;                 // 16-row MFMA blocks per wave
-constexpr uint32_t kTileN = 128;                        // vocab ids per workgroup
-constexpr uint32_t kNBlk = kTileN / kWavesN / 16;       // 16-id MFMA blocks per wave
-constexpr uint32_t kStepK = 64;                         // k per step: two MFMA k-halves of 32
-constexpr uint32_t kRing = TSM_LM_RING;                 // weight steps in flight per thread
-constexpr uint32_t kASets = TSM_LM_ASETS;               // A steps held per wave (the one in use and those ahead)
-constexpr uint32_t kRowB = kStepK * 2 + 16;             // LDS bytes per weight row (16 B pad: no bank conflicts)
-constexpr uint32_t kBufB = kTileN * kRowB;              // one LDS weight buffer (18,432 B)
-constexpr uint32_t kChunks = kTileN * kStepK * 2 / 16 / kThreads;  // 16-byte weight chunks per thread per step
-static_assert(kChunks * kThreads * 16 == kTileN * kStepK * 2, "weight tile split");
+constexpr uint32_t kTileN = 128;              // vocab ids per workgroup
+constexpr uint32_t kStepK = 64;               // k per step: two MFMA k-halves of 32
+constexpr uint32_t kRing = 4;                 // weight steps in flight per thread
+constexpr uint32_t kASets = 2;                // A steps held per wave (the one in use and the next)
+constexpr uint32_t kRowB = kStepK * 2 + 16;   // LDS bytes per weight row (16 B pad: no bank conflicts)
+constexpr uint32_t kBufB = kTileN * kRowB;    // one LDS weight buffer (18,432 B)
 static_assert(kRing % kASets == 0, "A sets follow the ring slots");
 static_assert(kRing >= 3, "a step is staged two steps ahead");
+
+// A workgroup's shape: TM rows x kTileN ids, WM waves along the rows and WN
+// along the vocabulary (8 waves, two per SIMD).
+template <uint32_t TM, uint32_t WM, uint32_t WN>
+struct Tile {
+    static constexpr uint32_t kTileM = TM, kWavesM = WM, kWavesN = WN;
+    static constexpr uint32_t kThreads = 64 * WM * WN;
+    static constexpr uint32_t kRowsW = TM / WM;                // rows per wave
+    static constexpr uint32_t kMBlk = kRowsW / 16;             // 16-row MFMA blocks per wave
+    static constexpr uint32_t kNBlk = kTileN / WN / 16;        // 16-id MFMA blocks per wave
+    static constexpr uint32_t kChunks = kTileN * kStepK * 2 / 16 / kThreads;  // 16-byte weight chunks per thread per step
+    static_assert(kChunks * kThreads * 16 == kTileN * kStepK * 2, "weight tile split");
+    static_assert(kMBlk >= 1 && kNBlk >= 1 && kRowsW % 16 == 0, "whole MFMA blocks");
+};
+// Every shape gives a wave 32 rows; fewer rows per workgroup spread the
+// waves along the vocabulary instead, so that a small batch does not pay for
+// a 256-row tile's MFMA work.
+using Tile256 = Tile<256, 8, 1>;  // a wave owns 32 rows x 128 ids
+using Tile128 = Tile<128, 4, 2>;  // 32 rows x 64 ids
+using Tile64 = Tile<64, 2, 4>;    // 32 rows x 32 ids
+using Tile32 = Tile<32, 1, 8>;    // 32 rows x 16 ids (decoding)
 
 struct PrepArgs {
     const float* x;
@@ -204,8 +204,10 @@ __device__ __forceinline__ bf16x8 frag(const uint16_t* p) {
 // gridDim.y * 256 rows (the padding zero), so its loads need no bounds; the
 // weight rows past `vocab` are clamped to the last one and their results are
 // not stored.
-template <bool kSplit>
-__global__ __launch_bounds__(kThreads) void lm_gemm_kernel(GemmArgs a) {
+template <bool kSplit, class T>
+__global__ __launch_bounds__(T::kThreads) void lm_gemm_kernel(GemmArgs a) {
+    constexpr uint32_t kTileM = T::kTileM, kWavesM = T::kWavesM, kWavesN = T::kWavesN, kThreads = T::kThreads;
+    constexpr uint32_t kRowsW = T::kRowsW, kMBlk = T::kMBlk, kNBlk = T::kNBlk, kChunks = T::kChunks;
     __shared__ __align__(16) uint8_t lds[3 * kBufB];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t n0 = blockIdx.x * kTileN;
@@ -349,7 +351,9 @@ void set_err(char* err, size_t errlen, const char* fmt, ...) {
     va_end(ap);
 }
 
-uint32_t rows_pad(uint32_t rows) { return (rows + kTileM - 1u) / kTileM * kTileM; }
+// The workgroup tile's rows for a batch: the smallest tile that holds it, up to 256.
+uint32_t tile_rows(uint32_t rows) { return rows <= 32u ? 32u : rows <= 64u ? 64u : rows <= 128u ? 128u : 256u; }
+uint32_t rows_pad(uint32_t rows) { return (rows + tile_rows(rows) - 1u) / tile_rows(rows) * tile_rows(rows); }
 
 }  // namespace lm
 }  // namespace tsm
@@ -411,9 +415,17 @@ int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* no
     g.dim = dim;
     g.vocab = vocab;
     g.ld = ld;
-    const dim3 grid((vocab + tsm::lm::kTileN - 1u) / tsm::lm::kTileN, rp / tsm::lm::kTileM);
-    if (split) hipLaunchKernelGGL(tsm::lm::lm_gemm_kernel<true>, grid, dim3(tsm::lm::kThreads), 0, st, g);
-    else hipLaunchKernelGGL(tsm::lm::lm_gemm_kernel<false>, grid, dim3(tsm::lm::kThreads), 0, st, g);
+    const uint32_t tm = tsm::lm::tile_rows(rows);
+    const dim3 grid((vocab + tsm::lm::kTileN - 1u) / tsm::lm::kTileN, rp / tm);
+    auto launch = [&](auto tile) {
+        using T = decltype(tile);
+        if (split) hipLaunchKernelGGL((tsm::lm::lm_gemm_kernel<true, T>), grid, dim3(T::kThreads), 0, st, g);
+        else hipLaunchKernelGGL((tsm::lm::lm_gemm_kernel<false, T>), grid, dim3(T::kThreads), 0, st, g);
+    };
+    if (tm == 32u) launch(tsm::lm::Tile32{});
+    else if (tm == 64u) launch(tsm::lm::Tile64{});
+    else if (tm == 128u) launch(tsm::lm::Tile128{});
+    else launch(tsm::lm::Tile256{});
     e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "gemm launch failed: %s", hipGetErrorString(e)), 1;
     return 0;

@@ -72,12 +72,14 @@ def check(case, got, want, s, tol):
     assert np.all(err <= tol * s + 1e-30), case
 
 
-def test_one_hot_weights_pin_the_layout(oracle):
+@pytest.mark.parametrize("rows", [200, 70, 40, 20])
+def test_one_hot_weights_pin_the_layout(oracle, rows):
     """Row v of W picks activation (5v + 3) mod dim: logit (r, v) is then
-    xb[r][(5v + 3) mod dim].  Rows 70 (not a multiple of 16 or 64), vocab 333
-    (not a multiple of 128), a row stride of dim + 8 and an output row of
-    vocab + 5 columns."""
-    rows, dim, vocab = 70, 128, 333
+    xb[r][(5v + 3) mod dim].  Rows 200, 70, 40 and 20 (the 256-, 128-, 64-
+    and 32-row workgroup tiles, none a multiple of 16), vocab 333 (not a
+    multiple of 128), a row stride of dim + 8 and an output row of vocab + 5
+    columns."""
+    dim, vocab = 128, 333
     rng = np.random.default_rng(11)
     x = rng.normal(0, 1.5, (rows, dim)).astype(np.float32)
     g = rng.normal(1, 0.2, dim).astype(np.float32)
@@ -95,7 +97,8 @@ def test_one_hot_weights_pin_the_layout(oracle):
         assert np.all(err <= tol * np.abs(want) + 1e-30), (split, float(err.max()))
 
 
-@pytest.mark.parametrize("rows,dim,vocab", [(1, 64, 1), (7, 128, 1000), (64, 640, 4099), (300, 256, 2000)])
+@pytest.mark.parametrize("rows,dim,vocab", [(1, 64, 1), (7, 128, 1000), (64, 640, 4099), (100, 192, 700),
+                                             (300, 256, 2000)])
 def test_random_against_the_oracle(oracle, rows, dim, vocab):
     rng = np.random.default_rng(rows * 7919 + dim + vocab)
     x = rng.normal(0, 2.0, (rows, dim)).astype(np.float32)
