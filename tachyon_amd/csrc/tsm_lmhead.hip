@@ -14,9 +14,11 @@
 //                   that a wave's fragment load is 1 KB in one piece; rows
 //                   past `rows` up to the tile are zero.
 //   lm_gemm_kernel  logits = A W^T on v_mfma_f32_16x16x32_bf16.  A workgroup
-//                   (8 waves, two per SIMD) owns 256 rows x 128 vocab ids;
-//                   wave w the rows 32w..32w+31 (2 x 8 MFMA tiles of 16 x 16,
-//                   64 f32 accumulators per lane).  The weight tile of each
+//                   (8 waves, two per SIMD) owns R rows x 128 vocab ids, R
+//                   the smallest of 32, 64, 128, 256 that holds the batch
+//                   (Tile); each wave owns 32 rows and 128 / (8 / (R / 32))
+//                   ids (at R = 256: 2 x 8 MFMA tiles of 16 x 16, 64 f32
+//                   accumulators per lane).  The weight tile of each
 //                   k-step (128 ids x 64 k, 16 KB) is loaded cooperatively
 //                   four steps ahead into a register ring (2 x 16 B per thread
 //                   per step), staged into one of three LDS buffers two steps
@@ -26,8 +28,9 @@
 //                   L2) are loaded by each wave straight into registers one
 //                   step ahead.
 //
-// Measured at 256 rows x dim 4096 x vocab 151,936 (MI355X): 466 us (bf16
-// activations) and 676 us (split), against 175 us for the bytes at 8 TB/s.
+// Measured at 256 rows x dim 4096 x vocab 151,936 (MI355X): about 470 us
+// (bf16 activations) and 690 us (split), against 175 us for the bytes at
+// 8 TB/s; one row (decoding) about 270 us.
 // One wave per SIMD issues these MFMAs at about half the peak rate (a
 // microbenchmark of independent MFMAs: 52% with one wave, 76% with two),
 // hence the 8-wave workgroup; the loads of both operands, the LDS reads and
