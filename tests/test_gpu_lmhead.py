@@ -189,3 +189,21 @@ def test_logits_feed_the_sampler(oracle):
     torch.cuda.synchronize()
     assert ctx.status() == 0
     check(host, out.numpy(), oracle.sample_batch(host), "lm_head -> tsm_sample")
+
+
+def test_tile_boundaries(oracle):
+    """Rows on both sides of every tile change (32/33, 64/65, 128/129,
+    256/257, 513: several 256-row tiles), hidden sizes 896 and 3584 (not
+    powers of two) and vocabularies ending one id into, or one id short of,
+    a 128-id tile; every logit of every row within the split bound."""
+    rng = np.random.default_rng(77)
+    shapes = [(32, 896, 129), (33, 896, 255), (64, 192, 128), (65, 192, 383), (128, 3584, 257),
+              (129, 128, 1), (256, 64, 640), (257, 64, 641), (513, 128, 300)]
+    for rows, dim, vocab in shapes:
+        say(f"tile boundary rows={rows} dim={dim} vocab={vocab}")
+        x = rng.normal(0, 2.0, (rows, dim)).astype(np.float32)
+        g = rng.normal(1, 0.3, dim).astype(np.float32)
+        wb = bf16_bits(rng.normal(0, 0.05, (vocab, dim)).astype(np.float32))
+        want = oracle.lm_head(x, g, 1e-5, wb)
+        s = bound_s(wb, oracle.rmsnorm(x, g, 1e-5))
+        check(f"rows={rows} dim={dim} vocab={vocab}", run(x, g, 1e-5, wb, True), want, s, TOL_SPLIT)
