@@ -43,8 +43,11 @@ def lm_head(x, norm_w, eps: float, w, split: bool = True, out=None, workspace=No
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     if out is None:
         out = torch.empty(rows, vocab, dtype=torch.float32, device=x.device)
-    if out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1 or out.shape[0] < rows:
-        raise ValueError("out must be float32 [rows, >= vocab] with unit column stride")
+    if (out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1 or out.shape[0] < rows
+            or out.shape[1] < vocab or not out.is_cuda):
+        raise ValueError("out must be float32 [>= rows, >= vocab] on the GPU with unit column stride")
+    if workspace.numel() * workspace.element_size() < need or not workspace.is_cuda:
+        raise ValueError(f"workspace must hold {need} bytes on the GPU")
     err = _lib._err()
     s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
     rc = _lib.lib().tsm_lm_head(s, x.data_ptr(), x.stride(0), norm_w.data_ptr(), float(eps), w.data_ptr(), rows, dim,
