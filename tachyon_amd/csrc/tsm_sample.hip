@@ -1354,24 +1354,23 @@ __device__ __forceinline__ uint64_t wave_sort64(uint64_t v) {
 __device__ __forceinline__ uint64_t* lds_wsort() { return reinterpret_cast<uint64_t*>(lds_base() + kOffHist + 1024 + kWaveList * 8); }
 static_assert(1024 + 2 * kWaveList * 8 <= kBins * 12, "wave sort scratch fits the histogram region");
 
-// Sorts the keys of lanes < n (n <= 64, distinct) ascending: each lane counts
-// the smaller keys from scalar broadcasts of the others', then the keys
-// trade places through LDS.  Lanes >= n get ~0.
+// Sorts the keys of lanes < n (n <= 64, distinct) ascending: the keys go to
+// LDS, each lane counts the keys below its own with loads every lane makes
+// at the same address (one LDS access each, no readlane round trips), then
+// the keys trade places through LDS.  Lanes >= n get ~0.
 __device__ __forceinline__ uint64_t wave_sort_rank(uint64_t v, uint32_t n) {
     const uint32_t lane = lane_id();
+    uint64_t* t = lds_wsort();
+    t[lane] = lane < n ? v : ~0ull;  // a key past the list (~0) is never below a listed one
+    __builtin_amdgcn_wave_barrier();
     uint32_t rank = 0;
-    // eight lanes per step with constant lane indices (no loop-carried
-    // scalar index, no branch per lane); a key past the list (~0) is never
-    // below a listed one
     for (uint32_t j0 = 0; j0 < n; j0 += 8) {
 #pragma unroll
-        for (uint32_t i = 0; i < 8; i++) {
-            const uint64_t o = (static_cast<uint64_t>(wave_read(static_cast<uint32_t>(v >> 32), j0 + i)) << 32) |
-                               wave_read(static_cast<uint32_t>(v), j0 + i);
-            rank += o < v ? 1u : 0u;
-        }
+        for (uint32_t i = 0; i < 8; i++) rank += t[j0 + i] < v ? 1u : 0u;
     }
-    uint64_t* t = lds_wsort();
+    // the wave's reads above complete before its writes below (LDS operations
+    // of one wave run in order)
+    __builtin_amdgcn_wave_barrier();
     if (lane < n) t[rank] = v;
     __builtin_amdgcn_wave_barrier();
     const uint64_t r = lane < n ? t[lane] : ~0ull;
@@ -1393,18 +1392,24 @@ __device__ __forceinline__ Pick wave_finalize(float y, uint32_t id, uint32_t len
         const uint64_t below = wave_ballot(lane < len && !(p >= P.min_p));
         if (below) len = max(static_cast<uint32_t>(__builtin_ctzll(below)), 1u);
     }
-    // The three folds run over the list in steps of eight lanes, without a
-    // branch per element: each records its running value in the lane of the
-    // element just added, and the first lane that meets a condition is found
-    // by ballot afterwards.  Past the list p is 0, which leaves a running sum
-    // as it is (sums of non-negative terms start from +0).
+    // The three folds run over the list in steps of eight elements, without a
+    // branch per element: every lane adds the same terms in list order (read
+    // from LDS at one address for all lanes), records the running value in
+    // the lane of the element just added, and the first lane that meets a
+    // condition is found by ballot afterwards.  Past the list p is 0, which
+    // leaves a running sum as it is (sums of non-negative terms start from
+    // +0).  The list's keys are in registers by now, so the sort's LDS words
+    // hold the terms.
     const float pl = lane < len ? p : 0.0f;
+    float* tp = reinterpret_cast<float*>(lds_wsort());  // [64] p, then [64] q
+    tp[lane] = pl;
+    __builtin_amdgcn_wave_barrier();
     // prefix sums (left fold) of p over the list
     float total = 0.0f, pre = 0.0f;
     for (uint32_t j0 = 0; j0 < len; j0 += 8) {
 #pragma unroll
         for (uint32_t i = 0; i < 8; i++) {
-            total += readlane_f(pl, j0 + i);
+            total += tp[j0 + i];
             pre = lane == j0 + i ? total : pre;
         }
     }
@@ -1412,11 +1417,13 @@ __device__ __forceinline__ Pick wave_finalize(float y, uint32_t id, uint32_t len
     if (!(m.greedy || P.top_p >= 1.0f)) {
         // the first j with q_0 + ... + q_j >= top_p (sampler.rs:240-246)
         const float q = lane < len ? pl / total : 0.0f;
+        tp[kWave + lane] = q;
+        __builtin_amdgcn_wave_barrier();
         float acc = 0.0f, accl = 0.0f;
         for (uint32_t j0 = 0; j0 < len; j0 += 8) {
 #pragma unroll
             for (uint32_t i = 0; i < 8; i++) {
-                acc += readlane_f(q, j0 + i);
+                acc += tp[kWave + j0 + i];
                 accl = lane == j0 + i ? acc : accl;
             }
         }
@@ -1431,10 +1438,11 @@ __device__ __forceinline__ Pick wave_finalize(float y, uint32_t id, uint32_t len
     for (uint32_t j0 = 0; j0 < keep; j0 += 8) {
 #pragma unroll
         for (uint32_t i = 0; i < 8; i++) {
-            r -= readlane_f(pl, j0 + i);
+            r -= tp[j0 + i];
             rl = lane == j0 + i ? r : rl;
         }
     }
+    __builtin_amdgcn_wave_barrier();  // the terms are read before the next sort reuses the words
     const uint64_t hit = wave_ballot(lane < keep && rl <= 0.0f);
     if (hit) pick = static_cast<uint32_t>(__builtin_ctzll(hit));
     Pick out;
