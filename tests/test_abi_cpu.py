@@ -103,8 +103,12 @@ def test_argument_errors_need_no_device():
 def test_lm_head_arguments_are_checked_on_the_host():
     L = _lib.lib()
     err = ctypes.create_string_buffer(256)
-    # workspace: the bf16 operands of the rows padded to 256, twice when split
-    assert L.tsm_lm_head_workspace(1, 4096, 0) == 256 * 4096 * 2
+    # workspace: the bf16 operands of the rows padded to the workgroup tile
+    # (32, 64, 128 or 256 rows), twice when split
+    assert L.tsm_lm_head_workspace(1, 4096, 0) == 32 * 4096 * 2
+    assert L.tsm_lm_head_workspace(33, 4096, 0) == 64 * 4096 * 2
+    assert L.tsm_lm_head_workspace(100, 4096, 0) == 128 * 4096 * 2
+    assert L.tsm_lm_head_workspace(256, 4096, 0) == 256 * 4096 * 2
     assert L.tsm_lm_head_workspace(257, 4096, _lib.LM_SPLIT) == 512 * 4096 * 2 * 2
     fake = ctypes.c_void_p(0x10000)  # never dereferenced: every case below fails its checks first
     def call(rows=4, dim=128, vocab=100, flags=0, ws=1 << 20, ld=100, x_stride=128, w=fake):
