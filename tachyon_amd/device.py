@@ -118,7 +118,10 @@ class SamplerContext:
             self._h = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library's module state may be gone already
+            pass
 
     def _batch(self, b: DeviceBatch, uniforms=True):
         return _lib.TsmBatch(
