@@ -94,13 +94,24 @@ size_t or_top_n(const float* x, size_t len, size_t n, float* vals, uint32_t* ids
     for (size_t i = 0; i < len; i++) {
         float v = x[i];
         if (k < n || v > floor) {
-            // partition_point(|&(w, _)| w >= v)
-            size_t lo = 0, hi = k;
-            while (lo < hi) {
-                size_t mid = lo + (hi - lo) / 2;
-                if (vals[mid] >= v) lo = mid + 1; else hi = mid;
+            // partition_point(|&(w, _)| w >= v), probing as the reference's
+            // toolchain does (Rust 1.87.0, pinned by .github/workflows/ci.yml:16-17,
+            // :64-65): partition_point is binary_search_by with `w >= v` as
+            // Less, whose loop runs while size > 1 { half = size / 2; mid =
+            // base + half; pred(mid) moves base to mid; size -= half } and
+            // returns base + pred(base).  With a NaN in the list the
+            // predicate is not monotone and only this probe order gives the
+            // reference's position.
+            size_t at = 0;
+            if (k > 0) {
+                size_t size = k, base = 0;
+                while (size > 1) {
+                    const size_t half = size / 2, mid = base + half;
+                    if (vals[mid] >= v) base = mid;
+                    size -= half;
+                }
+                at = base + (vals[base] >= v ? 1 : 0);
             }
-            size_t at = lo;
             if (k == n) k--;  // out.pop()
             std::memmove(vals + at + 1, vals + at, (k - at) * sizeof(float));
             std::memmove(ids + at + 1, ids + at, (k - at) * sizeof(uint32_t));

@@ -8,13 +8,14 @@
 // parallel selections of the sampling kernels assume a total order, so a row
 // whose logits hold a NaN is sampled here instead, element by element in id
 // order, with the insertion and the binary search done as the reference does
-// them.  The probe sequence is the halving search of Rust's
-// slice::binary_search_by as it stood before its 2024 rewrite (lo = 0, hi =
-// len; mid = lo + (hi - lo) / 2; the predicate moves lo past mid or hi down
-// to mid), which the oracle restates; the rewritten search probes other
-// positions, so on such rows the reference's own output depends on the
-// toolchain it is built with (it pins none).  Such a row is pathological
-// (one wave walks the whole row), so nothing here is tuned.
+// them.  The probe sequence is that of slice::binary_search_by in Rust
+// 1.87.0, the toolchain the reference's CI pins (.github/workflows/ci.yml:16-17,
+// :64-65): size = len, base = 0; while size > 1 { half = size / 2; mid = base
+// + half; the predicate moves base to mid; size -= half }; the position is
+// base + pred(base).  The oracle restates the same order (the older halving
+// search probes other positions and keeps other ids on such rows).  Such a
+// row is pathological (one wave walks the whole row), so nothing here is
+// tuned.
 //
 // Also in the reference's order: argmax (sampler.rs:314-322, the first index
 // that nothing after it beats: 0 when x[0] is NaN), the mask filter and the
@@ -126,14 +127,17 @@ __device__ __noinline__ inline uint32_t top_n_ref(const Row& r, const Lds& s, ui
                 if (!cand) break;
                 const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(cand));
                 const float v = lane_f(y, l);
-                // partition_point(|&(w, _)| w >= v)
-                uint32_t lo = 0, hi = k;
-                while (lo < hi) {
-                    const uint32_t mid = lo + (hi - lo) / 2u;
-                    if (s.val[mid] >= v) lo = mid + 1u;
-                    else hi = mid;
+                // partition_point(|&(w, _)| w >= v) in Rust 1.87.0's probe order
+                uint32_t at = 0;
+                if (k) {
+                    uint32_t size = k, b = 0;
+                    while (size > 1u) {
+                        const uint32_t half = size / 2u, mid = b + half;
+                        if (s.val[mid] >= v) b = mid;
+                        size -= half;
+                    }
+                    at = b + (s.val[b] >= v ? 1u : 0u);
                 }
-                const uint32_t at = lo;
                 if (k == want) k--;  // out.pop()
                 // out.insert(at, ..): entries [at, k) move up one, top chunk first
                 for (uint32_t c = k; c > at;) {
@@ -197,7 +201,9 @@ __device__ __noinline__ inline uint32_t fallback_ref(const Row& r, const Lds& s,
                 const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(cand));
                 const uint64_t v = (static_cast<uint64_t>(wave_read(static_cast<uint32_t>(me >> 32), l)) << 32) |
                                    wave_read(static_cast<uint32_t>(me), l);
-                uint32_t lo = 0, hi = k;  // composites are distinct: a plain lower bound
+                // composites are distinct and totally ordered: any probe order
+                // gives the same lower bound
+                uint32_t lo = 0, hi = k;
                 while (lo < hi) {
                     const uint32_t mid = lo + (hi - lo) / 2u;
                     if (s.comp[mid] < v) lo = mid + 1u;

@@ -47,8 +47,10 @@ constexpr uint32_t kOffGH = kOffHCnt + kHSlots * 4;           // u32[3][256] his
 constexpr uint32_t kOffMisc = kOffGH + 3 * 256 * 4;           // u32[64]
 constexpr uint32_t kOffTmp = kOffMisc + 64 * 4;               // u32[64] reduction scratch
 constexpr uint32_t kOffTmpD = kOffTmp + 64 * 4;               // f64[16]
+constexpr uint32_t kRedW = 16;                                // words per wave in a reduction area
+constexpr uint32_t kOffRed = kOffTmpD + 16 * 8;               // u32[2][kSW][kRedW] reduction areas
 constexpr uint32_t kListMax = kMaxWindow;                     // ranked list entries
-constexpr uint32_t kOffLY = kOffTmpD + 16 * 8;                // u32[kListMax] y bits (sorted list)
+constexpr uint32_t kOffLY = kOffRed + 2 * kSW * kRedW * 4;    // u32[kListMax] y bits (sorted list)
 constexpr uint32_t kOffLI = kOffLY + kListMax * 4;            // u32[kListMax] ids
 constexpr uint32_t kOffLP = kOffLI + kListMax * 4;            // f32[kListMax] p_j
 constexpr uint32_t kOffLQ = kOffLP + kListMax * 4;            // u64[kListMax] unsorted composites
@@ -79,10 +81,12 @@ static_assert(kOffLY % 16 == 0, "float4 staging alignment");
 
 // Per-wave partial results meet in LDS at a few barriers only: each wave
 // reduces its values with DPP and lane 0 files them in s_red (kRedW words per
-// wave); after the barrier every thread reads the waves' words.
-constexpr uint32_t kRedW = 16;
-__device__ __forceinline__ uint32_t* s_red(int k) { return s_tmp() + k * kSW * kRedW; }  // k = 0 or 1 (two areas)
-static_assert(2 * kSW * kRedW <= 64 + 64 + 32, "reduction areas fit tmp + tmpd");
+// wave); after the barrier every thread reads the waves' words.  The two
+// areas have LDS of their own: a wave that has read them may go on to write
+// the scratch words and the staging slots while another still reads.
+__device__ __forceinline__ uint32_t* s_red(int k) {  // k = 0 or 1 (two areas)
+    return reinterpret_cast<uint32_t*>(lds_base() + kOffRed) + k * kSW * kRedW;
+}
 
 // misc[] slots
 enum : uint32_t {
@@ -1483,22 +1487,34 @@ __global__ __launch_bounds__(kSB) void split_kernel(SplitArgs a) {
     uint32_t seg_flags = nan_seg ? SEG_NAN : 0u;
     uint32_t pen_off = 0;
     uint2* const rcand = a.w.cand + static_cast<size_t>(row) * a.nseg * kCandCap;  // the row's area
+    // ---- the staged slots' elements that pass, counted: a segment writes
+    // at most kCandCap entries (the row's area holds kCandCap per segment),
+    // so a segment whose count exceeds it takes the exact thresholds below.
+    // The count can: the staging holds up to kSW * kFStage * 4 elements, and
+    // with fewer finite group maxima than `need` every element passes ----
+    const bool two = tal == tal && tal < tall;
+    const bool tal_all = two && !(tal > -INFINITY);
+    auto pass = [&](float x, uint32_t nb, int c, uint32_t e) {
+        const bool al = (nb >> c) & 1u;
+        if (e >= hi) return false;
+        return x >= tall || (two && al && (tal_all || x >= tal));
+    };
+    uint32_t mine = 0;
     if (!ovf) {
-        // ---- the staged slots' elements that pass, counted, reserved per
-        // wave and written ----
-        const bool two = tal == tal && tal < tall;
-        const bool tal_all = two && !(tal > -INFINITY);
-        auto pass = [&](float x, uint32_t nb, int c, uint32_t e) {
-            const bool al = (nb >> c) & 1u;
-            if (e >= hi) return false;
-            return x >= tall || (two && al && (tal_all || x >= tal));
-        };
-        uint32_t mine = 0;
         for (uint32_t j = lane; j < fpos; j += kWave) {
             const float4 x = fst[j];
             const uint32_t f = fid[j], e0 = f & kIdMask, nb = f >> 24;
             mine += pass(x.x, nb, 0, e0) + pass(x.y, nb, 1, e0 + 1) + pass(x.z, nb, 2, e0 + 2) + pass(x.w, nb, 3, e0 + 3);
         }
+        const uint32_t wn = wave_sum_dpp(mine);
+        if (lane == 0) s_tmp()[56 + wid] = wn;
+        TSM_LDS_SYNC();  // ovf is the same in every thread: a uniform barrier
+        uint32_t seg_total = 0;
+#pragma unroll
+        for (int w = 0; w < kSW; w++) seg_total += s_tmp()[56 + w];
+        ovf = seg_total > kCandCap;
+    }
+    if (!ovf) {
         // one reservation per wave for its candidates and its history entries
         const uint32_t wn = wave_sum_dpp(mine), wh = m.penal ? wave_sum_dpp(nh) : 0u;
         uint64_t prev = 0;
@@ -1522,9 +1538,12 @@ __global__ __launch_bounds__(kSB) void split_kernel(SplitArgs a) {
         }
         if (!two) tal_out = mrow ? tall : kNaNf;
     } else {
-        // too many for the staging area (ties): exact thresholds by radix
-        // selection, and the entries written straight from the row in memory
-        // into a reservation of kCandCap (unused slots skipped)
+        // too many for the staging area or for the segment's candidate area
+        // (ties, or too few group maxima to bound it): exact thresholds by
+        // radix selection, and the entries written straight from the row in
+        // memory into a reservation of kCandCap (unused slots skipped).  At
+        // most need[0] + need[1] <= 2 * kSplitNeed entries pass them.
+        static_assert(2 * kSplitNeed <= kCandCap, "the exact thresholds' entries fit a segment's area");
         seg_flags |= SEG_EXACT;
         const uint64_t ca = seg_select_exact(rowp, mrow, lo, hi, need[0], false);
         const uint64_t cl = mrow ? seg_select_exact(rowp, mrow, lo, hi, need[1], true) : 0ull;

@@ -230,11 +230,12 @@ CONFIGS = {"c1": c1, "c2": c2, "c3": c3, "c4": c4, "c5": c5}
 
 def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, mask_frac=0.3,
                 logprobs=True, hist_len=16, penalties=True, mode="mixed", sigma=2.0, outlier=None,
-                specials=False):
+                specials=False, nan_frac=0.0):
     """Small random workload for parity tests: mixed per-row settings, optional
     heavy ties (integer-valued logits), masks and histories.  `outlier` sets
     id 0 of every row to that value (a narrow cluster of logits next to one
-    far value); `specials` puts NaN, +inf and -inf logits into the rows."""
+    far value); `specials` puts NaN, +inf and -inf logits into the rows;
+    `nan_frac` makes that fraction of every row's ids NaN."""
     rng = np.random.default_rng(seed)
     stride = stride or vocab
     if ties:
@@ -263,6 +264,9 @@ def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, 
             else:
                 x[r, srng.integers(0, vocab, 1)] = np.inf
                 x[r, srng.integers(0, vocab, 2)] = np.nan
+    if nan_frac > 0.0:
+        nrng = np.random.default_rng(seed + 9999)
+        x[:, :vocab][nrng.random((rows, vocab)) < nan_frac] = np.nan
     p = make_params(rows)
     for r in range(rows):
         kind = mode if mode != "mixed" else ["greedy", "topk", "topp", "nucleus", "minp", "all"][r % 6]
@@ -301,6 +305,30 @@ def random_case(seed, rows=8, vocab=300, stride=None, ties=False, masked=False, 
         mask = pack_mask(allowed)
     top_stride = 20 if logprobs else 0
     return Workload(f"rand{seed}", x, vocab, p, ids, offs, mask, uniforms(rng, rows), top_stride=top_stride)
+
+
+def window_case(seed, vocab, rows=1, top_k=1024, hist_len=10, repetition_penalty=1.3, masked=False,
+                mask_frac=0.5, sigma=2.0):
+    """Top-k windows near their 1024 limit over small vocabularies: a
+    segment of the split-row kernel then has fewer finite group maxima than
+    the window needs, and every one of its elements is a candidate.  Rows
+    take top_k, top_k - 24, ... so a batch holds several window sizes; each
+    row's history is `hist_len` distinct ids, penalized by
+    `repetition_penalty`."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, vocab)) * sigma).astype(np.float32)
+    p = make_params(rows, temperature=0.8, top_p=1.0, repetition_penalty=repetition_penalty)
+    for r in range(rows):
+        p["top_k"][r] = max(1, top_k - 24 * r)
+        if masked:
+            p["flags"][r] |= ROW_CONSTRAINED
+        if r % 2:
+            p["flags"][r] |= ROW_LOGPROBS
+            p["n_logprobs"][r] = 5
+    ids = np.concatenate([rng.choice(vocab, hist_len, replace=False) for _ in range(rows)]).astype(np.uint32)
+    offs = (np.arange(rows + 1) * hist_len).astype(np.uint32)
+    mask = pack_mask(rng.random((rows, vocab)) < mask_frac) if masked else None
+    return Workload(f"window{seed}", x, vocab, p, ids, offs, mask, uniforms(rng, rows), top_stride=8)
 
 
 # ---- JSON-object constraints (mask producer) ----------------------------------

@@ -124,6 +124,11 @@ RANDOM_CASES = [
     dict(seed=20, vocab=3000, rows=20, specials=True, masked=True),
     dict(seed=24, vocab=3000, rows=12, specials=True, mode="topk", masked=True, mask_frac=0.02),
     dict(seed=25, vocab=5000, rows=20, specials=True, mode="nucleus"),
+    # rows with NaNs at 3-5% of their ids, where partition_point's probe
+    # order decides which ids top_n keeps (the split-row kernel: 12 rows;
+    # the whole-row kernel: 20 rows)
+    dict(seed=30, vocab=2000, rows=12, nan_frac=0.05, mode="topk"),
+    dict(seed=31, vocab=3000, rows=20, nan_frac=0.03, mode="topk", masked=True),
     # histories longer than the LDS history table (2048 ids): penalties
     # applied on re-reads
     dict(seed=26, vocab=3000, rows=20, hist_len=4000),
@@ -138,3 +143,10 @@ DIST_CASES = [(21, dict(vocab=500, mode="mixed")), (22, dict(vocab=3000, mode="m
               (23, dict(vocab=3000, mode="topk", ties=True)),
               # kept sets beyond the 1024 written entries (DIST_TRUNCATED)
               (28, dict(vocab=6000, mode="nucleus", sigma=0.5))]
+
+# Top-k windows near 1024 over vocabularies a few segments long: with fewer
+# finite group maxima than the window needs, every element of a split-row
+# segment passes its threshold (more than a segment's candidate area holds)
+WINDOW_CASES = [dict(seed=40, vocab=4000), dict(seed=41, vocab=8192, hist_len=8),
+                dict(seed=42, vocab=6000, rows=4, hist_len=400, masked=True),
+                dict(seed=43, vocab=12000, rows=3, top_k=1000, hist_len=500, repetition_penalty=0.9)]

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import emu_harness as E
-from parity import DIST_CASES, RANDOM_CASES, check, check_distribution, check_mask_property
+from parity import DIST_CASES, RANDOM_CASES, WINDOW_CASES, check, check_distribution, check_mask_property
 from tachyon_amd import workloads as wl
 
 # the small cases run here; the wide ones (vocab >= 20000, and nucleus rows
@@ -50,6 +50,14 @@ def test_emu_parity_random(case):
 @pytest.mark.parametrize("case", WIDE, ids=[f"rand{c['seed']}" for c in WIDE])
 def test_emu_parity_random_wide(case):
     run_case(wl.random_case(**case), f"emu rand{case['seed']}")
+
+
+@pytest.mark.parametrize("case", WINDOW_CASES, ids=[f"window{c['seed']}" for c in WINDOW_CASES])
+def test_emu_parity_wide_windows(case):
+    """Split-row segments whose candidates would exceed the segment's area
+    (regression: such a segment wrote past it, into other segments' entries
+    and beyond the scratch) take the exact thresholds instead."""
+    run_case(wl.window_case(**case), f"emu window{case['seed']}")
 
 
 @pytest.mark.parametrize("name,rows", [("c1", 1), ("c2", 8), ("c3", 4), ("c4", 4), ("c5", 4)])

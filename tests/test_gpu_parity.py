@@ -22,7 +22,7 @@ from tachyon_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
 
-from parity import DIST_CASES, RANDOM_CASES, check, check_distribution, check_mask_property
+from parity import DIST_CASES, RANDOM_CASES, WINDOW_CASES, check, check_distribution, check_mask_property
 
 
 def say(msg):
@@ -103,6 +103,13 @@ def test_parity_random(ctx, case):
         big.close()
 
 
+@pytest.mark.parametrize("case", WINDOW_CASES, ids=[f"window{c['seed']}" for c in WINDOW_CASES])
+def test_parity_wide_windows(ctx, case):
+    """Top-k windows near 1024 over small vocabularies: split-row segments
+    whose candidates exceed the segment's area take the exact thresholds."""
+    run_case(ctx, wl.window_case(**case), f"window{case['seed']}")
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
 def test_parity_baseline_configs(ctx, name):
     w = wl.CONFIGS[name]()
@@ -121,6 +128,13 @@ def _rows_of(w, sel, name):
     return wl.Workload(name, np.ascontiguousarray(w.logits[sel]), w.usable, w.params[sel].copy(), hist_ids, hist_off,
                        None if w.mask is None else np.ascontiguousarray(w.mask[sel]), w.uniforms[sel].copy(),
                        top_stride=w.top_stride)
+
+
+@pytest.mark.parametrize("case", WINDOW_CASES, ids=[f"window{c['seed']}" for c in WINDOW_CASES])
+def test_parity_wide_windows(ctx, case):
+    """Top-k windows near 1024 over small vocabularies: split-row segments
+    whose candidates exceed the segment's area take the exact thresholds."""
+    run_case(ctx, wl.window_case(**case), f"window{case['seed']}")
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])

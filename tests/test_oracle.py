@@ -418,8 +418,10 @@ def test_boundary_check_rejects_exact_arithmetic_picks(oracle):
 
 def test_nan_and_inf_semantics_hand_derived(oracle):
     """NaN and infinite logits, traced by hand through sampler.rs: top_n's
-    insertion with partition_point (the halving search: mid = lo + (hi - lo)
-    / 2, lo = mid + 1 while w >= v holds), `v > floor` false for NaN, argmax's
+    insertion with partition_point in the probe order of Rust 1.87.0, the
+    reference's pinned toolchain (size = len, base = 0; while size > 1: half
+    = size / 2, mid = base + half, base = mid when w >= v holds, size -=
+    half; then base + [w(base) >= v]), `v > floor` false for NaN, argmax's
     strict '>', NaN probabilities that no fold step decides, and pick
     falling through to idx[keep - 1] (sampler.rs:139-150, :267-285, :314-322)."""
     nan, inf = np.nan, np.inf
@@ -435,6 +437,22 @@ def test_nan_and_inf_semantics_hand_derived(oracle):
     # -> 5 > floor 1: probes 3 >= 5 no, NaN >= 5 no -> [5, NaN, 3]
     v, i = oracle.top_n([3.0, nan, 1.0, 5.0], 3)
     assert i.tolist() == [3, 1, 0] and v[0] == 5.0 and np.isnan(v[1]) and v[2] == 3.0
+    # [6, NaN, 7, 9, 6, 5, 6], n=6, where the probe orders differ:
+    # [6] -> [NaN, 6] -> 7: probe 6 (no), base NaN (no): [7, NaN, 6]
+    # -> 9: probes NaN, NaN, base 7 (no): [9, 7, NaN, 6]
+    # -> 6 (id 4): size 4 probes NaN (no), size 2 probes 7 (yes, base 1),
+    #    base 7 >= 6: at 2: [9, 7, 6, NaN, 6]
+    # -> 5: size 5 probes 6 (yes, base 2), size 3 and 2 probe NaN (no),
+    #    base 6 >= 5: at 3: [9, 7, 6, 5, NaN, 6], full, floor 6 (id 0)
+    # -> 6 (id 6): 6 > 6 is false, skipped.  (The older halving search puts
+    #    5 last, floor 5, and then inserts id 6: [3, 2, 4, 6, 1, 0].)
+    v, i = oracle.top_n([6.0, nan, 7.0, 9.0, 6.0, 5.0, 6.0], 6)
+    assert i.tolist() == [3, 2, 4, 5, 1, 0] and np.isnan(v[4])
+    # [1, NaN, 2, 3, 0.5], n=4: [1] -> [NaN, 1] -> 2: probe 1 (no), base
+    # NaN (no): [2, NaN, 1] -> 3: probes NaN, NaN, base 2 (no): at 0:
+    # [3, 2, NaN, 1], full, floor 1: 0.5 is never inserted
+    v, i = oracle.top_n([1.0, nan, 2.0, 3.0, 0.5], 4)
+    assert i.tolist() == [3, 2, 1, 0]
     # [0, inf, 1, inf], n=3: ties of inf keep the lower id first
     v, i = oracle.top_n([0.0, inf, 1.0, inf], 3)
     assert i.tolist() == [1, 3, 2]
