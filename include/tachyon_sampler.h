@@ -167,19 +167,31 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
                      char* err, size_t errlen);
 
 /*
- * Waits for the context's last call and returns its device-side status:
+ * Waits for the context's last call (an event on that call's stream; other
+ * streams are not waited for) and returns the device-side status:
  * 0 when every row was sampled by the specified rule, otherwise TSM_STATUS_*
  * bits (e.g. a history row longer than TSM_MAX_HISTORY, whose counts are
  * then capped, or a row whose n_logprobs exceeds top_stride, whose list is
- * then cut to top_stride).  Clears the status.
+ * then cut to top_stride).  Clears the status.  A call queued on the context
+ * while tsm_status() runs races with the clearing (a context serves one
+ * caller at a time).
  */
 #define TSM_STATUS_HISTORY_TOO_LONG 1u
 #define TSM_STATUS_BAD_PARAMS       2u
 #define TSM_STATUS_DIST_TRUNCATED   4u
-#define TSM_STATUS_INTERNAL         8u /* a selection found no element (not
-                                          expected: rows holding NaN or
+#define TSM_STATUS_INTERNAL         8u /* a row the device could not sample
+                                          exactly; token 0 and keep 0
+                                          written.  Rows holding NaN or
                                           infinite logits are sampled as the
-                                          reference does); token 0 written */
+                                          reference does.  Known case: a row
+                                          without top-k whose candidates hold
+                                          more than three dense clusters, each
+                                          narrower than 1/2048 of the row's
+                                          value span and with more distinct
+                                          values near one fold event than the
+                                          exact folds' census takes (2048).
+                                          Fallback: sample that row with the
+                                          CPU Sampler, as INTEGRATION.md says */
 #define TSM_STATUS_ROW_KIND        16u /* a row of a kind the batch's row_kinds
                                           left out: token 0 written           */
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);

@@ -14,6 +14,13 @@ struct tsm_ctx {
     uint32_t* status;  // TSM_STATUS_* bits of the calls since the last tsm_status()
     void* split_mem;   // the split kernel's scratch (tsm::split::SplitScratch)
     tsm::split::SplitScratch split;
+    // tsm_status() waits for the last call through an event on that call's
+    // stream and reads the status on a stream of the context's own (created
+    // non-blocking, default priority), so it stalls no other stream
+    hipEvent_t last;
+    bool called;
+    hipStream_t own;
+    uint32_t* host_word;  // pinned: the status word read back
 };
 
 namespace {
@@ -164,7 +171,14 @@ tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err
     c->max_vocab = max_vocab;
     c->status = nullptr;
     c->split_mem = nullptr;
+    c->last = nullptr;
+    c->called = false;
+    c->own = nullptr;
+    c->host_word = nullptr;
     hipError_t e = hipMalloc(&c->status, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->last, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->host_word), sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
     // the split kernel runs for batches of at most kSplitRowsMax rows
     const uint32_t split_rows = max_rows < tsm::split::kSplitRowsMax ? max_rows : tsm::split::kSplitRowsMax;
@@ -188,6 +202,9 @@ void tsm_destroy(tsm_ctx* ctx) {
     (void)hipDeviceSynchronize();
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->split_mem) (void)hipFree(ctx->split_mem);
+    if (ctx->last) (void)hipEventDestroy(ctx->last);
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    if (ctx->host_word) (void)hipHostFree(ctx->host_word);
     delete ctx;
 }
 
@@ -256,8 +273,13 @@ static int run(tsm_ctx* ctx, void* stream, const tsm_batch* b, const tsm_outputs
     if (check_batch(ctx->max_rows, ctx->max_vocab, b, err, errlen)) return 1;
     DeviceGuard g(ctx->device);
     if (!g.ok) return set_err(err, errlen, "hipSetDevice(%d) failed", ctx->device), 1;
-    return queue(static_cast<hipStream_t>(stream), b, out, dist_ids, dist_probs, dist_stride, keep, distribution,
-                 ctx->status, &ctx->split, err, errlen);
+    if (queue(static_cast<hipStream_t>(stream), b, out, dist_ids, dist_probs, dist_stride, keep, distribution,
+              ctx->status, &ctx->split, err, errlen))
+        return 1;
+    const hipError_t e = hipEventRecord(ctx->last, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return set_err(err, errlen, "hipEventRecord failed: %s", hipGetErrorString(e)), 1;
+    ctx->called = true;
+    return 0;
 }
 
 int tsm_sample(tsm_ctx* ctx, void* stream, const tsm_batch* batch, const tsm_outputs* out, char* err,
@@ -283,10 +305,13 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch, uint32_
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen) {
     if (!ctx || !status) return set_err(err, errlen, "context or status is NULL"), 1;
     DeviceGuard g(ctx->device);
-    hipError_t e = hipDeviceSynchronize();
-    if (e == hipSuccess) e = hipMemcpy(status, ctx->status, sizeof(uint32_t), hipMemcpyDeviceToHost);
-    if (e == hipSuccess) e = hipMemset(ctx->status, 0, sizeof(uint32_t));
+    hipError_t e = ctx->called ? hipEventSynchronize(ctx->last) : hipSuccess;
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(ctx->host_word, ctx->status, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->own);
+    if (e == hipSuccess) e = hipMemsetAsync(ctx->status, 0, sizeof(uint32_t), ctx->own);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->own);
     if (e != hipSuccess) return set_err(err, errlen, "status read failed: %s", hipGetErrorString(e)), 1;
+    *status = *ctx->host_word;
     return 0;
 }
 

@@ -69,7 +69,13 @@ constexpr uint32_t kOffESort = kOffEHMin + kHS * 4;      // u64[kHS] bucket sort
 constexpr uint32_t kOffERunP = kOffESort + kHS * 8;      // f32[kHS] run probabilities
 constexpr uint32_t kOffEExp = kOffERunP + kHS * 4;       // u64[32] the expf table
 constexpr uint32_t kOffESHi = kOffEExp + 32 * 8;         // f32[kNB] total's value at bin starts, ties up
-constexpr uint32_t kOffEEnd = kOffESHi + kNB * 4;
+// crowded coarse bins (see FBins): a count, kCrowd coarse bin ids, then each
+// one's cumulative-count table at its kSub + 1 sub-bin edges
+constexpr uint32_t kCrowd = 3;
+constexpr uint32_t kSub = 256;
+constexpr uint32_t kOffECrowd = kOffESHi + kNB * 4;      // u32[4]: slots used, coarse bins
+constexpr uint32_t kOffECdf = kOffECrowd + 16;           // u16[kCrowd][kSub + 1] sub-bin edges' CDF (of 65535)
+constexpr uint32_t kOffEEnd = kOffECdf + ((kCrowd * (kSub + 1) * 2 + 7) & ~7u);
 static_assert(kOffEMass % 8 == 0 && kOffEScd % 8 == 0 && kOffESort % 8 == 0 && kOffEExp % 8 == 0,
               "8-byte LDS records");
 static_assert(kOffEEnd <= kOffMisc, "engine LDS overlaps the row's scalars");
@@ -100,6 +106,10 @@ __device__ __forceinline__ uint64_t* e_sort() { return reinterpret_cast<uint64_t
 __device__ __forceinline__ uint32_t* e_rbin() { return e_u32(kOffESort); }
 __device__ __forceinline__ float* e_runp() { return reinterpret_cast<float*>(lds_base() + kOffERunP); }
 __device__ __forceinline__ uint64_t* e_exptab() { return reinterpret_cast<uint64_t*>(lds_base() + kOffEExp); }
+__device__ __forceinline__ uint32_t* e_crowd() { return e_u32(kOffECrowd); }
+__device__ __forceinline__ uint16_t* e_cdf(uint32_t slot) {
+    return reinterpret_cast<uint16_t*>(lds_base() + kOffECdf) + slot * (kSub + 1u);
+}
 
 enum : uint32_t {  // e_sc() words
     SC_FIRST = 0,   // first nonempty bin
@@ -203,15 +213,38 @@ __device__ __forceinline__ uint64_t wave_read64(uint64_t v, uint32_t lane) {
 // (fine bins keep the list order), equal values share a bin, and a value
 // spread that is even inside each coarse bin gives each fine bin about len /
 // kNB candidates.  e_lay()[c] = C(c); scale = kNB / len (0: fine = coarse).
+//
+// A coarse bin whose values are far from even inside it (a dense cluster
+// narrower than the bin) can leave one fine bin more candidates than a census
+// round takes.  Such a bin (crowded: up to kCrowd of them, cr[]) is laid out
+// from a histogram of its own: fr is replaced by the bin's cumulative count
+// at fr, interpolated linearly between its kSub sub-bin edges, so its fine
+// bins hold about equal counts at the sub-bin's resolution.  The map stays
+// monotone in y (the edges' counts never fall) and a function of y alone.
+__device__ __forceinline__ float crowd_frac(const uint16_t* F, float fr) {
+    const float x = fr * static_cast<float>(kSub);
+    const uint32_t j = x < static_cast<float>(kSub - 1u) ? static_cast<uint32_t>(x) : kSub - 1u;
+    const float w = x - static_cast<float>(j);  // in [0, 1]
+    const float a = static_cast<float>(F[j]), b = static_cast<float>(F[j + 1u]);
+    const float v = (a + w * (b - a)) * (1.0f / 65535.0f);
+    return v < 1.0f ? v : 1.0f;
+}
 struct FBins {
     VBins vb;
     float scale;
+    uint32_t cr[kCrowd];  // crowded coarse bins laid out from their own sub-histogram (kNoBin: none)
+    __device__ __forceinline__ float frac(float y, uint32_t c) const {
+        const float fr = vb.pos(y) - static_cast<float>(c);
+        return fr > 0.0f ? (fr < 1.0f ? fr : 1.0f) : 0.0f;
+    }
     __device__ __forceinline__ uint32_t bin(float y) const {
         const uint32_t c = vb.bin(y);
         if (scale == 0.0f) return c;
         const uint32_t c0 = e_lay()[c], c1 = c + 1u < kNB ? e_lay()[c + 1u] : c0 + (kNB - 1u);
-        float fr = vb.pos(y) - static_cast<float>(c);
-        fr = fr > 0.0f ? (fr < 1.0f ? fr : 1.0f) : 0.0f;
+        float fr = frac(y, c);
+#pragma unroll
+        for (uint32_t s = 0; s < kCrowd; s++)
+            if (c == cr[s]) fr = crowd_frac(e_cdf(s), fr);
         const float v = (static_cast<float>(c0) + fr * static_cast<float>(c1 - c0)) * scale;
         return v >= static_cast<float>(kNB - 1u) ? kNB - 1u : static_cast<uint32_t>(v);
     }
@@ -660,7 +693,7 @@ __device__ __forceinline__ void add_term(uint32_t slot, uint32_t b, float tau, i
     }
 }
 
-enum : int { EP_HIST = 0, EP_SR = 1, EP_A = 2, EP_CENSUS = 3 };
+enum : int { EP_HIST = 0, EP_SR = 1, EP_A = 2, EP_CENSUS = 3, EP_SUB = 4 };
 
 // One re-read of the row for the engine, its candidates (filter q, in total
 // order) handled by mode:
@@ -668,7 +701,9 @@ enum : int { EP_HIST = 0, EP_SR = 1, EP_A = 2, EP_CENSUS = 3 };
 //              smallest candidate's key, whether a candidate is NaN;
 //   EP_SR      the grid sums of total and the draw, and the census;
 //   EP_A       the grid sums of acc (terms p / T), and the census;
-//   EP_CENSUS  the census alone.
+//   EP_CENSUS  the census alone;
+//   EP_SUB     the crowded coarse bins' sub-histograms (kSub bins each, in
+//              e_hkey, which holds no census yet).
 // The row is read as in row_pass (16-byte blocks, the next tile in flight);
 // each element takes one predicate and one branch into the mode's work.
 template <int kMode>
@@ -686,6 +721,8 @@ __device__ __noinline__ void eng_pass(Fin& f_in, const Filt& q_in, const FBins& 
             e_sc()[SC_NAN] = 0u;
             e_sc()[SC_CMIN] = 0xFFFFFFFFu;
         }
+    } else if (kMode == EP_SUB) {
+        for (uint32_t i = tid; i < kCrowd * kSub; i += kBlock) e_hkey()[i] = 0u;
     } else if (kMode == EP_SR || kMode == EP_A) {
         const uint32_t nslot = kMode == EP_SR ? 4u : 2u;
         for (uint32_t i = tid; i < nslot * kNB; i += kBlock) e_sum(0)[i] = 0u;
@@ -766,6 +803,19 @@ __device__ __noinline__ void eng_pass(Fin& f_in, const Filt& q_in, const FBins& 
                 if (q.use_minp && keep) {
                     keep = !(y < q.minp_lo);
                     if (keep && !(y >= q.minp_hi)) keep = glibc_expf_lds((y - q.y0) / t, tab) >= q.minp;
+                }
+                if (kMode == EP_SUB) {
+                    if (keep && y == y) {
+                        const uint32_t c = vb.vb.bin(y);
+#pragma unroll
+                        for (uint32_t s = 0; s < kCrowd; s++) {
+                            if (c != vb.cr[s]) continue;
+                            const float x = vb.frac(y, c) * static_cast<float>(kSub);
+                            const uint32_t j = x < static_cast<float>(kSub - 1u) ? static_cast<uint32_t>(x) : kSub - 1u;
+                            atomicAdd(&e_hkey()[s * kSub + j], 1u);
+                        }
+                    }
+                    continue;
                 }
                 const uint32_t b = vb.bin(y);
                 if (kMode == EP_HIST) {
@@ -1234,6 +1284,102 @@ __device__ uint32_t last_agree(uint32_t limit) {
     return r;
 }
 
+// After the fine layout's histogram: the coarse bins (this thread's two,
+// with cnt0 / cnt1 candidates) holding a part of a fine bin with more
+// candidates than a census round takes are crowded; up to kCrowd of them get
+// a sub-histogram (one more pass) and are laid out from it (FBins).  Returns
+// whether any was, so that the caller counts the fine bins again.
+__device__ __noinline__ bool crowd_layout(Fin& f, const Filt& q, FBins& vb, uint32_t cnt0, uint32_t cnt1) {
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) e_crowd()[0] = 0u;
+    TSM_LDS_SYNC();
+#pragma unroll
+    for (uint32_t k = 0; k < 2u; k++) {
+        const uint32_t c = 2u * tid + k;
+        if ((k == 0u ? cnt0 : cnt1) <= kReqCnt / 4u) continue;  // too few to crowd a fine bin
+        const uint32_t l0 = e_lay()[c], l1 = c + 1u < kNB ? e_lay()[c + 1u] : l0 + (kNB - 1u);
+        const uint32_t f0 = min(static_cast<uint32_t>(static_cast<float>(l0) * vb.scale), kNB - 1u);
+        const uint32_t f1 = min(static_cast<uint32_t>(static_cast<float>(l1) * vb.scale), kNB - 1u);
+        bool crowded = false;
+        for (uint32_t j = f0; j <= f1 && !crowded; j++) crowded = e_cnt()[j] > kReqCnt;
+        if (crowded) {
+            const uint32_t sl = atomicAdd(&e_crowd()[0], 1u);
+            if (sl < kCrowd) e_crowd()[1u + sl] = c;
+        }
+    }
+    TSM_LDS_SYNC();
+    const uint32_t nc = min(e_crowd()[0], kCrowd);
+    if (nc == 0u) return false;
+#pragma unroll
+    for (uint32_t sl = 0; sl < kCrowd; sl++) vb.cr[sl] = sl < nc ? e_crowd()[1u + sl] : kNoBin;
+    // the sub-histograms (by the coarse bins and fr only), then each crowded
+    // bin's cumulative counts at its sub-bin edges, wave sl for slot sl
+    eng_pass<EP_SUB>(f, q, vb, 0.0f);
+    const uint32_t wid = tid / kWave, lane = lane_id();
+    if (wid < nc) {
+        constexpr uint32_t kPerLane = kSub / kWave;
+        static_assert(kPerLane * kWave == kSub, "sub-bins per lane");
+        uint32_t h[kPerLane], sum = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < kPerLane; i++) {
+            h[i] = e_hkey()[wid * kSub + lane * kPerLane + i];
+            sum += h[i];
+        }
+        const uint32_t incl = wave_incl_scan(sum);
+        const uint32_t n = wave_read(incl, kWave - 1u);
+        uint16_t* F = e_cdf(wid);
+        uint32_t cum = incl - sum;
+#pragma unroll
+        for (uint32_t i = 0; i < kPerLane; i++) {
+            const uint32_t j = lane * kPerLane + i;
+            F[j] = static_cast<uint16_t>(n ? (static_cast<uint64_t>(cum) * 65535u) / n : (j * 65535u) / kSub);
+            cum += h[i];
+        }
+        if (lane == 0) F[kSub] = 65535u;
+    }
+    TSM_LDS_SYNC();
+    return true;
+}
+
+// Sampler::distribution (sampler.rs:102-116) for a kept set of `keep`
+// candidates (filter q, `len` candidates before the kept count): the first
+// min(keep, stride) of them, best first, as (id, p_j / mass), written in
+// chunks of up to kExactCap entries, each selected above the previous one's
+// last composite, gathered and sorted.  Returns the best id (0 when nothing
+// was written).
+__device__ __noinline__ uint32_t write_dist_chunks(Fin& f, const Filt& q, uint32_t len, uint32_t keep,
+                                                   const DistOut* dist, float y0, float t, float mass) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t k = min(keep, dist->stride);
+    uint32_t done = 0, best = 0;
+    uint64_t last = 0;
+    while (done < k) {
+        const uint32_t c = min(k - done, kExactCap);
+        Filt qd = q;
+        if (done) {
+            qd.use_min = true;
+            qd.min_comp = last;
+        }
+        if (done + c < len) {
+            qd.use_max = true;
+            qd.max_comp = select_kth(f, qd, c);
+        }
+        const uint32_t g = gather_pass(f, qd, kExactCap);
+        if (g == 0u) break;
+        sort_gathered(f, g);
+        last = f.gcomp()[g - 1u];
+        if (done == 0u) best = f.rid()[0];
+        for (uint32_t j = tid; j < g; j += kBlock) {
+            dist->ids[done + j] = f.rid()[j];
+            dist->probs[done + j] = glibc_expf((f.ry()[j] - y0) / t) / mass;
+        }
+        done += g;
+        TSM_LDS_SYNC();  // every thread has read gcomp before the next chunk's passes
+    }
+    if (keep > done && tid == 0) atomicOr(dist->status, TSM_STATUS_DIST_TRUNCATED);
+    return best;
+}
+
 struct BigOut {
     Pick pick;
     bool small;  // at most kExactCap candidates: the caller finishes them exactly
@@ -1261,6 +1407,8 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     TSM_LDS_SYNC();
     FBins vb;
     vb.vb.y0 = y0;
+#pragma unroll
+    for (uint32_t sl = 0; sl < kCrowd; sl++) vb.cr[sl] = kNoBin;
     {
         float span = fminf(30.5f, (y0 - mlo) / t);
         if (!(span > 0.0f)) span = 1.0f;
@@ -1320,6 +1468,7 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
             vb.scale = static_cast<float>(kNB) / static_cast<float>(wtot);
             TSM_LDS_SYNC();
             eng_pass<EP_HIST>(f, q, vb, 0.0f);
+            if (crowd_layout(f, q, vb, c0, c1)) eng_pass<EP_HIST>(f, q, vb, 0.0f);
         }
         if (!degenerate && len <= kExactCap) {
             out.small = true;
@@ -1342,22 +1491,7 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
         out.pick.token = static_cast<uint32_t>(last);
         out.pick.mass = __uint_as_float(0x7FC00000u);
         out.pick.prob = out.pick.mass;
-        if (dist) {
-            const uint32_t k = min(min(len, dist->stride), kExactCap);
-            Filt qd = q;
-            if (k < len) {
-                qd.use_max = true;
-                qd.max_comp = select_kth(f, q, k);
-            }
-            const uint32_t g = gather_pass(f, qd, kExactCap);
-            sort_gathered(f, g);
-            for (uint32_t j = tid; j < g; j += kBlock) {
-                dist->ids[j] = f.rid()[j];
-                dist->probs[j] = glibc_expf((f.ry()[j] - y0) / t) / out.pick.mass;
-            }
-            if (len > g && tid == 0) atomicOr(dist->status, TSM_STATUS_DIST_TRUNCATED);
-            TSM_LDS_SYNC();
-        }
+        if (dist) write_dist_chunks(f, q, len, len, dist, y0, t, out.pick.mass);
         return out;
     }
     // total's (and the draw's) plans, sums and census
@@ -1466,21 +1600,7 @@ __device__ __noinline__ BigOut big_nucleus(Fin& f_in, const Filt& q_in, float y0
     out.pick.keep = keep;
     out.pick.mass = mass;
     if (dist) {  // Sampler::distribution (sampler.rs:102-116): the kept candidates over mass
-        const uint32_t k = min(min(keep, dist->stride), kExactCap);
-        Filt qd = q;
-        if (k < len) {
-            qd.use_max = true;
-            qd.max_comp = select_kth(f, q, k);
-        }
-        const uint32_t g = gather_pass(f, qd, kExactCap);
-        sort_gathered(f, g);
-        for (uint32_t j = tid; j < g; j += kBlock) {
-            dist->ids[j] = f.rid()[j];
-            dist->probs[j] = glibc_expf((f.ry()[j] - y0) / t) / mass;
-        }
-        if (keep > g && tid == 0) atomicOr(dist->status, TSM_STATUS_DIST_TRUNCATED);
-        out.pick.token = g > 0 ? f.rid()[0] : 0u;
-        TSM_LDS_SYNC();
+        out.pick.token = write_dist_chunks(f, q, len, keep, dist, y0, t, mass);
         return out;
     }
     // the draw (sampler.rs:142-150)

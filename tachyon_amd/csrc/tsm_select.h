@@ -78,9 +78,11 @@ struct Filt {
     bool need_allowed = false;
     bool use_cut = false;
     bool use_max = false;
+    bool use_min = false;  // composites above min_comp only (a chunk after the ones before it)
     bool use_minp = false;
     float cut = 0.0f;
     uint64_t max_comp = ~0ull;
+    uint64_t min_comp = 0ull;
     float y0 = 0.0f;
     float minp = 0.0f;
     // min-p band: y >= minp_hi is kept and y < minp_lo dropped without the
@@ -135,6 +137,7 @@ __device__ __forceinline__ bool keep_el(const Fin& f, const Filt& q, uint32_t id
     if (q.need_allowed && !allowed_bit(f, id)) return false;
     if (q.use_cut && !(y >= q.cut)) return false;
     if (q.use_max && c > q.max_comp) return false;
+    if (q.use_min && c <= q.min_comp) return false;
     if (q.use_minp) {
         if (y < q.minp_lo) return false;
         if (!(y >= q.minp_hi) && !(glibc_expf((y - q.y0) / f.m.t) >= q.minp)) return false;

@@ -331,6 +331,54 @@ def window_case(seed, vocab, rows=1, top_k=1024, hist_len=10, repetition_penalty
     return Workload(f"window{seed}", x, vocab, p, ids, offs, mask, uniforms(rng, rows), top_stride=8)
 
 
+def cluster_case(seed, vocab=151936, rows=4, width=0.025, temperature=3.0, top_p=0.9, sigma=3.0):
+    """Nucleus rows (no top-k) whose first third of the vocabulary sits in a
+    dense Gaussian cluster about `width` wide at 3.0, beside N(0, sigma^2)
+    logits: at a high temperature every id is a candidate and one value bin
+    of the cluster holds thousands of them."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, vocab)) * sigma).astype(np.float32)
+    k = vocab // 3
+    x[:, :k] = (3.0 + rng.standard_normal((rows, k)) * (width / 6.0)).astype(np.float32)
+    p = make_params(rows, temperature=temperature, top_k=0, top_p=top_p)
+    p["repetition_penalty"][1::2] = 1.1
+    ids, offs = uniform_histories(rng, rows, 64, vocab)
+    return Workload(f"cluster{seed}", x, vocab, p, ids, offs, None, uniforms(rng, rows))
+
+
+def sweep_batch(seed, rows=32):
+    """One batch of the seeded GPU sweep: a vocabulary size, a logit
+    distribution (Gaussian of several widths, bf16-like quantized values with
+    many equal logits, one far outlier per row, a dense cluster over a third
+    of the row), per-row temperature, top-k (none, inside and beyond the
+    1024-entry window), top-p, min-p, penalties and, for some batches, a mask
+    with constrained rows.  Returns (workload, distribution kind)."""
+    rng = np.random.default_rng(seed)
+    V = int(rng.choice([3000, 20000, 60000, 151936]))
+    sig = float(rng.choice([0.3, 1.0, 2.0, 3.0, 6.0]))
+    x = (rng.standard_normal((rows, V)) * sig).astype(np.float32)
+    kind = int(rng.integers(0, 5))
+    if kind == 1:
+        x = (np.round(x * 8) / 8).astype(np.float32)
+    elif kind == 2:
+        x[np.arange(rows), rng.integers(0, V, rows)] += np.float32(rng.uniform(2, 15))
+    elif kind == 3:
+        x[:, :V // 3] = (x[:, :V // 3] * 0.001 + 3).astype(np.float32)
+    p = make_params(rows, temperature=1.0, top_k=0, top_p=1.0)
+    p["temperature"] = rng.choice([0.3, 0.7, 1.0, 1.5, 3.0], rows).astype(np.float32)
+    p["top_p"] = rng.choice([0.5, 0.9, 0.95, 0.99, 1.0], rows).astype(np.float32)
+    p["top_k"] = rng.choice([0, 0, 0, 50, 2000, 5000], rows).astype(np.uint32)
+    p["presence_penalty"] = np.where(rng.random(rows) < 0.2, 0.3, 0.0).astype(np.float32)
+    p["min_p"] = np.where(rng.random(rows) < 0.2, 0.01, 0.0).astype(np.float32)
+    p["repetition_penalty"] = np.where(rng.random(rows) < 0.3, 1.1, 1.0).astype(np.float32)
+    ids, off = uniform_histories(rng, rows, 64, V)
+    mask = None
+    if rng.random() < 0.3:
+        mask = pack_mask(rng.random((rows, V)) < rng.uniform(0.05, 0.9))
+        p["flags"] = np.where(rng.random(rows) < 0.5, ROW_CONSTRAINED, 0).astype(np.uint32)
+    return Workload(f"sweep{seed}", x, V, p, ids, off, mask, uniforms(rng, rows)), kind
+
+
 # ---- JSON-object constraints (mask producer) ----------------------------------
 
 def _pick_bytes(rng, alphabet, n):

@@ -428,6 +428,32 @@ hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d) {
 }
 hipError_t hipDeviceSynchronize() { return hipSuccess; }
 hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) {
+    *s = reinterpret_cast<hipStream_t>(std::malloc(16));
+    return *s ? hipSuccess : hipErrorOutOfMemory;
+}
+hipError_t hipStreamDestroy(hipStream_t s) {
+    std::free(s);
+    return hipSuccess;
+}
+hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) {
+    *e = reinterpret_cast<hipEvent_t>(std::malloc(16));
+    return *e ? hipSuccess : hipErrorOutOfMemory;
+}
+hipError_t hipEventDestroy(hipEvent_t e) {
+    std::free(e);
+    return hipSuccess;
+}
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t) { return e ? hipSuccess : hipErrorInvalidValue; }
+hipError_t hipEventSynchronize(hipEvent_t e) { return e ? hipSuccess : hipErrorInvalidValue; }
+hipError_t hipHostMalloc(void** p, size_t n, unsigned) {
+    *p = std::malloc(n);
+    return *p ? hipSuccess : hipErrorOutOfMemory;
+}
+hipError_t hipHostFree(void* p) {
+    std::free(p);
+    return hipSuccess;
+}
 hipError_t hipGetLastError() { return hipSuccess; }
 const char* hipGetErrorString(hipError_t e) { return e == hipSuccess ? "hipSuccess" : "emulated HIP error"; }
 hipError_t hipFuncSetAttribute(const void*, hipFuncAttribute a, int v) {

@@ -279,6 +279,9 @@ typedef enum hipError_t {
     hipErrorLaunchFailure = 719,
 } hipError_t;
 typedef struct ihipStream_t* hipStream_t;
+typedef struct ihipEvent_t* hipEvent_t;
+constexpr unsigned hipEventDisableTiming = 2u;
+constexpr unsigned hipStreamNonBlocking = 1u;
 enum hipMemcpyKind { hipMemcpyHostToHost, hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice,
                      hipMemcpyDefault };
 enum hipFuncAttribute { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
@@ -303,6 +306,15 @@ hipError_t hipGetDevice(int* d);
 hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d);
 hipError_t hipDeviceSynchronize();
 hipError_t hipStreamSynchronize(hipStream_t s);
+// streams and events: the emulation runs every launch to completion at once
+hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned flags);
+hipError_t hipStreamDestroy(hipStream_t s);
+hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned flags);
+hipError_t hipEventDestroy(hipEvent_t e);
+hipError_t hipEventRecord(hipEvent_t e, hipStream_t s = nullptr);
+hipError_t hipEventSynchronize(hipEvent_t e);
+hipError_t hipHostMalloc(void** p, size_t n, unsigned flags = 0);
+hipError_t hipHostFree(void* p);
 hipError_t hipGetLastError();
 const char* hipGetErrorString(hipError_t e);
 hipError_t hipFuncSetAttribute(const void* f, hipFuncAttribute a, int v);

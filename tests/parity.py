@@ -150,3 +150,24 @@ DIST_CASES = [(21, dict(vocab=500, mode="mixed")), (22, dict(vocab=3000, mode="m
 WINDOW_CASES = [dict(seed=40, vocab=4000), dict(seed=41, vocab=8192, hist_len=8),
                 dict(seed=42, vocab=6000, rows=4, hist_len=400, masked=True),
                 dict(seed=43, vocab=12000, rows=3, top_k=1000, hist_len=500, repetition_penalty=0.9)]
+
+
+def dense_cluster_workloads():
+    """Nucleus rows (no top-k, T 2-3) whose first third of the vocabulary is
+    a dense cluster narrower than one value bin: two rows of the seeded sweep
+    (batches 193 and 272) that once ended with INTERNAL (a fine bin beyond a
+    census round), and eight synthetic rows of the same kind with other
+    top-p and temperatures.  Returns [(label, workload)]."""
+    out = []
+    for b, r in [(193, 7), (272, 18)]:
+        w, _ = wl.sweep_batch(0x5EE0 + b)
+        ids = w.hist_ids[w.hist_offsets[r]:w.hist_offsets[r + 1]]
+        out.append((f"sweep{b} row {r}",
+                    wl.Workload(f"sweep{b}r{r}", w.logits[r:r + 1].copy(), w.usable, w.params[r:r + 1].copy(),
+                                ids.copy(), np.array([0, len(ids)], np.uint32), None,
+                                w.uniforms[r:r + 1].copy(), w.top_stride)))
+    w = wl.cluster_case(seed=60, vocab=151936, rows=8)
+    w.params["temperature"] = np.array([3, 3, 3, 2, 3, 3, 2.5, 3], np.float32)
+    w.params["top_p"] = np.array([1.0, 0.9, 0.99, 1.0, 0.95, 1.0, 0.9, 0.5], np.float32)
+    out.append(("cluster60", w))
+    return out

@@ -94,26 +94,31 @@ def test_emu_distribution():
         check_distribution(w, got["ids"], got["probs"], got["keep"], rids, rps, rkeep, f"emu dist{seed}")
 
 
-# Known limit of the exact nucleus folds: a fine bin whose candidates exceed
-# what one census round takes (1024 candidates, 2048 distinct values), even
-# censused alone, ends its row with TSM_STATUS_INTERNAL and token 0.  The two
-# rows below, from an extended run of the GPU sweep (993 batches of 32 rows:
-# these two rows reported the status, every other row was bit-exact), carry
-# a third of the vocabulary in a cluster 0.025 wide at T = 3 with no top-k;
-# the equal-count fine bins split the cluster's coarse bin linearly by value
-# and one of them receives 2582 candidates.  Strict: once the folds handle
-# such a bin, these pass and the marker must go.
-@pytest.mark.xfail(strict=True, reason="a fine bin beyond one census round ends the row with INTERNAL")
-@pytest.mark.parametrize("batch,row", [(193, 7), (272, 18)])
-def test_emu_dense_cluster_beyond_the_census(batch, row):
+def test_emu_distribution_whole_kept_set():
+    """Kept sets of thousands written whole in chunks of 1024, best first."""
     from oracle import pyoracle
-    from test_gpu_sweep import sweep_batch
 
-    w, _ = sweep_batch(0x5EE0 + batch)
-    ids = w.hist_ids[w.hist_offsets[row]:w.hist_offsets[row + 1]]
-    w1 = wl.Workload(f"sweep{batch}r{row}", w.logits[row:row + 1].copy(), w.usable, w.params[row:row + 1].copy(),
-                     ids.copy(), np.array([0, len(ids)], np.uint32), None, w.uniforms[row:row + 1].copy(),
-                     w.top_stride)
-    got = E.emu_sample(w1)
+    w = wl.random_case(seed=28, rows=3, vocab=6000, mode="nucleus", sigma=0.5)
+    got = E.emu_distribution(w, 8192)
+    rids, rps, rkeep = pyoracle.distribution_batch(w, 8192)
+    assert (rkeep > 1024).all(), rkeep
+    check_distribution(w, got["ids"], got["probs"], got["keep"], rids, rps, rkeep, "emu dist28 whole")
+    assert got["status"] & 4 == 0
+
+
+# Nucleus rows with a dense cluster narrower than a value bin: the fine bins
+# of such a coarse bin are laid out from its own sub-histogram, so that no
+# fine bin holds more candidates than a census round takes (these rows ended
+# with INTERNAL before)
+@pytest.mark.parametrize("idx", [0, 1, 2], ids=["sweep193r7", "sweep272r18", "cluster60"])
+def test_emu_dense_cluster(idx):
+    from oracle import pyoracle
+
+    if idx == 2 and not ALL:
+        pytest.skip("eight rows of 151,936 candidates take minutes on the emulation; TSM_EMU_ALL=1 runs them")
+    from parity import dense_cluster_workloads
+
+    label, w = dense_cluster_workloads()[idx]
+    got = E.emu_sample(w)
     assert got["status"] == 0, got["status"]
-    check(w1, got, pyoracle.sample_batch(w1), f"emu sweep{batch} row {row}")
+    check(w, got, pyoracle.sample_batch(w), f"emu {label}")

@@ -110,6 +110,15 @@ def test_parity_wide_windows(ctx, case):
     run_case(ctx, wl.window_case(**case), f"window{case['seed']}")
 
 
+def test_parity_dense_clusters(ctx):
+    """Nucleus rows whose dense cluster once overflowed a census round
+    (sweep batches 193 and 272) and eight synthetic rows of that kind."""
+    from parity import dense_cluster_workloads
+
+    for label, w in dense_cluster_workloads():
+        run_case(ctx, w, label)
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
 def test_parity_baseline_configs(ctx, name):
     w = wl.CONFIGS[name]()
@@ -135,6 +144,15 @@ def test_parity_wide_windows(ctx, case):
     """Top-k windows near 1024 over small vocabularies: split-row segments
     whose candidates exceed the segment's area take the exact thresholds."""
     run_case(ctx, wl.window_case(**case), f"window{case['seed']}")
+
+
+def test_parity_dense_clusters(ctx):
+    """Nucleus rows whose dense cluster once overflowed a census round
+    (sweep batches 193 and 272) and eight synthetic rows of that kind."""
+    from parity import dense_cluster_workloads
+
+    for label, w in dense_cluster_workloads():
+        run_case(ctx, w, label)
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
@@ -217,6 +235,29 @@ def test_distribution_parity(ctx):
         # a kept set beyond the written entries is reported
         st = ctx.status()
         assert bool(st & 4) == bool((rkeep > 1024).any()), (seed, st)
+
+
+@pytest.mark.parametrize("seed,vocab,stride", [(28, 6000, 8192), (32, 40000, 16384), (33, 151936, 4096)])
+def test_distribution_parity_whole_kept_set(ctx, seed, vocab, stride):
+    """Kept sets of thousands of candidates (nucleus rows over N(0, 0.5^2)
+    logits) written whole, best first, up to the stride: every entry equals
+    the oracle's Sampler::distribution; the truncation bit is set exactly when
+    a kept count exceeds the stride."""
+    import torch
+
+    from oracle import pyoracle
+    from tachyon_amd.device import upload
+
+    ctx.status()
+    w = wl.random_case(seed=seed, rows=6, vocab=vocab, mode="nucleus", sigma=0.5)
+    say(f"[gpu] distribution seed {seed}: V={vocab}, stride {stride}")
+    ids, ps, keep = ctx.distribution(upload(w), stride)
+    torch.cuda.synchronize()
+    ids, ps, keep = ids.cpu().numpy().view(np.uint32), ps.cpu().numpy(), keep.cpu().numpy().view(np.uint32)
+    rids, rps, rkeep = pyoracle.distribution_batch(w, stride)
+    assert (rkeep > 1024).all(), rkeep  # every row's kept set is beyond one chunk
+    check_distribution(w, ids, ps, keep, rids, rps, rkeep, f"dist{seed}")
+    assert bool(ctx.status() & 4) == bool((rkeep > stride).any()), seed
 
 
 def test_abi_rejects_bad_arguments(ctx):

@@ -10,36 +10,9 @@ import sys
 import numpy as np
 import pytest
 
-from tachyon_amd import workloads as wl
+from tachyon_amd.workloads import sweep_batch
 
 pytestmark = pytest.mark.gpu
-
-
-def sweep_batch(seed, rows=32):
-    rng = np.random.default_rng(seed)
-    V = int(rng.choice([3000, 20000, 60000, 151936]))
-    sig = float(rng.choice([0.3, 1.0, 2.0, 3.0, 6.0]))
-    x = (rng.standard_normal((rows, V)) * sig).astype(np.float32)
-    kind = int(rng.integers(0, 5))
-    if kind == 1:
-        x = (np.round(x * 8) / 8).astype(np.float32)
-    elif kind == 2:
-        x[np.arange(rows), rng.integers(0, V, rows)] += np.float32(rng.uniform(2, 15))
-    elif kind == 3:
-        x[:, :V // 3] = (x[:, :V // 3] * 0.001 + 3).astype(np.float32)
-    p = wl.make_params(rows, temperature=1.0, top_k=0, top_p=1.0)
-    p["temperature"] = rng.choice([0.3, 0.7, 1.0, 1.5, 3.0], rows).astype(np.float32)
-    p["top_p"] = rng.choice([0.5, 0.9, 0.95, 0.99, 1.0], rows).astype(np.float32)
-    p["top_k"] = rng.choice([0, 0, 0, 50, 2000, 5000], rows).astype(np.uint32)
-    p["presence_penalty"] = np.where(rng.random(rows) < 0.2, 0.3, 0.0).astype(np.float32)
-    p["min_p"] = np.where(rng.random(rows) < 0.2, 0.01, 0.0).astype(np.float32)
-    p["repetition_penalty"] = np.where(rng.random(rows) < 0.3, 1.1, 1.0).astype(np.float32)
-    ids, off = wl.uniform_histories(rng, rows, 64, V)
-    mask = None
-    if rng.random() < 0.3:
-        mask = wl.pack_mask(rng.random((rows, V)) < rng.uniform(0.05, 0.9))
-        p["flags"] = np.where(rng.random(rows) < 0.5, wl.ROW_CONSTRAINED, 0).astype(np.uint32)
-    return wl.Workload(f"sweep{seed}", x, V, p, ids, off, mask, wl.uniforms(rng, rows)), kind
 
 
 def test_seeded_sweep_matches_the_oracle():
