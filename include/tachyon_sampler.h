@@ -109,8 +109,11 @@ typedef struct tsm_batch {
  * its parameters, the batch's `usable`, the row's history length and whether
  * the batch has a mask.
  */
-#define TSM_ROWKIND_SPLIT 1u
-#define TSM_ROWKIND_WHOLE 2u
+#define TSM_ROWKIND_SPLIT 1u /* the split-row kernel (batches of up to 16 rows)      */
+#define TSM_ROWKIND_WHOLE 2u /* the general whole-row kernel                         */
+#define TSM_ROWKIND_LEAN  4u /* the lean whole-row kernel: top-k rows with at most
+                                64 kept ids and penalties that only lower values
+                                (a split row of a larger batch takes it too)       */
 
 /* One step's outputs.  `token` is required; every other pointer may be NULL. */
 typedef struct tsm_outputs {
@@ -212,9 +215,11 @@ int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);
 int tsm_sample_static(void* stream, const tsm_batch* batch, const tsm_outputs* out,
                       uint32_t* status, char* err, size_t errlen);
 
-/* The kind (TSM_ROWKIND_*) of a row: `p` is the row's parameters (host
+/* The kinds (TSM_ROWKIND_* bits) of a row: `p` is the row's parameters (host
  * memory), `usable` the batch's, `hist_len` the row's history length,
- * `has_mask` whether the batch passes a mask. */
+ * `has_mask` whether the batch passes a mask.  TSM_ROWKIND_SPLIT when the
+ * split-row kernel takes the row in a small batch, and TSM_ROWKIND_LEAN or
+ * TSM_ROWKIND_WHOLE for the whole-row kernel that takes it otherwise. */
 uint32_t tsm_row_kind(const tsm_row_params* p, uint32_t usable, uint32_t hist_len, int has_mask);
 
 /*

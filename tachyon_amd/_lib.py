@@ -74,6 +74,7 @@ SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_s
 LM_SPLIT = 1
 ROWKIND_SPLIT = 1
 ROWKIND_WHOLE = 2
+ROWKIND_LEAN = 4
 
 _lib = None
 

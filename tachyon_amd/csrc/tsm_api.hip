@@ -61,7 +61,7 @@ int check_batch(uint32_t max_rows, uint32_t max_vocab, const tsm_batch* b, char*
         return set_err(err, errlen, "batch->usable %u exceeds row_stride %u", b->usable, b->row_stride), 1;
     if ((b->hist_ids == nullptr) != (b->hist_offsets == nullptr))
         return set_err(err, errlen, "hist_ids and hist_offsets must both be set or both be NULL"), 1;
-    if (b->row_kinds & ~(TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE))
+    if (b->row_kinds & ~(TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE | TSM_ROWKIND_LEAN))
         return set_err(err, errlen, "batch->row_kinds 0x%x has unknown bits", b->row_kinds), 1;
     if (b->reserved != 0) return set_err(err, errlen, "batch->reserved must be 0"), 1;
     if (b->mask && b->mask_stride < (b->usable + 31) / 32)
@@ -134,7 +134,8 @@ const char* tsm_version(void) { return "tachyon-sampler 0.2 gfx950"; }
 uint32_t tsm_row_kind(const tsm_row_params* p, uint32_t usable, uint32_t hist_len, int has_mask) {
     if (!p || usable == 0) return TSM_ROWKIND_WHOLE;
     const tsm::RowMode m = tsm::row_mode(*p, usable, hist_len, has_mask != 0);
-    return tsm::split::takes_row(m, hist_len) ? TSM_ROWKIND_SPLIT : TSM_ROWKIND_WHOLE;
+    const uint32_t whole = tsm::lean_takes(m, *p, hist_len, usable, false) ? TSM_ROWKIND_LEAN : TSM_ROWKIND_WHOLE;
+    return (tsm::split::takes_row(m, hist_len) ? TSM_ROWKIND_SPLIT : 0u) | whole;
 }
 
 tsm_ctx* tsm_create(int device, uint32_t max_rows, uint32_t max_vocab, char* err, size_t errlen) {
@@ -242,24 +243,33 @@ static int queue(hipStream_t s, const tsm_batch* b, const tsm_outputs* out, uint
         a.out_prob = out->prob;
         a.out_keep = out->keep;
     }
-    // one kernel per row kind the batch holds (both when it does not say).
-    // The split-row kernel pays off for small batches, where one workgroup
-    // per row would leave most of the chip idle; from kSplitRowsMax rows on,
-    // the whole-row kernel samples every row (it takes every kind).
-    uint32_t kinds = b->row_kinds ? b->row_kinds : (TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE);
-    if (b->rows > tsm::split::kSplitRowsMax || !split) kinds = TSM_ROWKIND_WHOLE;
+    // one kernel per row kind the batch holds (every kernel when it does not
+    // say).  The split-row kernel pays off for small batches, where one
+    // workgroup per row would leave most of the chip idle; from
+    // kSplitRowsMax rows on, the whole-row kernels sample every row.  The
+    // lean kernel takes the common top-k rows, the general kernel every
+    // other; distribution() always takes the general kernel.
+    uint32_t kinds = b->row_kinds ? b->row_kinds : (TSM_ROWKIND_SPLIT | TSM_ROWKIND_WHOLE | TSM_ROWKIND_LEAN);
+    if (b->rows > tsm::split::kSplitRowsMax || !split) {
+        // a split-kind row takes a whole-row kernel: the one its kind names
+        // beside SPLIT (kinds from tsm_row_kind always name one); a bare
+        // SPLIT says nothing more, so the general kernel takes it
+        if ((kinds & TSM_ROWKIND_SPLIT) && !(kinds & (TSM_ROWKIND_WHOLE | TSM_ROWKIND_LEAN))) kinds |= TSM_ROWKIND_WHOLE;
+        kinds &= ~TSM_ROWKIND_SPLIT;
+    }
+    if (distribution && (kinds & TSM_ROWKIND_LEAN)) kinds = (kinds & ~TSM_ROWKIND_LEAN) | TSM_ROWKIND_WHOLE;
     if (kinds & TSM_ROWKIND_SPLIT) {
         tsm::split::SplitArgs sa;
         sa.s = a;
         sa.w = *split;
         sa.seg_len = tsm::split::pick_seg_len(b->rows, b->usable);
         sa.nseg = (b->usable + sa.seg_len - 1) / sa.seg_len;
-        sa.general = (kinds & TSM_ROWKIND_WHOLE) ? 1u : 0u;
+        sa.general = (kinds & (TSM_ROWKIND_WHOLE | TSM_ROWKIND_LEAN)) ? 1u : 0u;
         tsm::split::launch(sa, b->rows, vec, s);
     }
-    if (kinds & TSM_ROWKIND_WHOLE) {
+    if (kinds & (TSM_ROWKIND_WHOLE | TSM_ROWKIND_LEAN)) {
         a.skip_split = (kinds & TSM_ROWKIND_SPLIT) ? 1u : 0u;
-        tsm::launch_sample(a, b->rows, vec, s);
+        tsm::launch_sample(a, b->rows, vec, (kinds & TSM_ROWKIND_LEAN) != 0u, (kinds & TSM_ROWKIND_WHOLE) != 0u, s);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "kernel launch failed: %s", hipGetErrorString(e)), 1;

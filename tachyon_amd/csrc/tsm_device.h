@@ -18,6 +18,10 @@ constexpr uint32_t kTile = kBlock * kVec * 4;  // 8192 ids per tile of the strea
 constexpr uint32_t kMaxWindow = 1024;  // top_n path bound (sampler.rs:193)
 constexpr uint32_t kWideWindow = 256;  // constrained window floor (sampler.rs:186-187)
 constexpr uint32_t kExactCap = 1024;   // longest ranked list finished exactly
+constexpr uint32_t kWaveList = 64;     // longest ranked list the single-wave finish takes
+constexpr uint32_t kBitmapWords = 8192;  // history bitmap: rows of up to 262144 ids
+constexpr uint32_t kHashSlots = 4096;    // history count table (histories up to kHistFast ids)
+constexpr uint32_t kHistFast = kHashSlots / 2;
 constexpr uint32_t kBins = 2048;       // radix histogram bins (11-bit digits)
 
 // ---- per-row mode (sampler.rs:161-190 + extensions) -------------------------

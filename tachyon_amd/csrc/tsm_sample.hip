@@ -46,7 +46,7 @@ enum : uint32_t {
 };
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;     // canon_key(-inf): a threshold every non-NaN value passes
 constexpr uint32_t kKeyUntracked = 0xFFFFFFFFu;  // threshold of a target not tracked: reads as NaN, keeps nothing
-constexpr uint32_t kBigEmit = 64;                // a wave's candidates in one tile past which it tightens first
+constexpr uint32_t kBigEmit = 64;                // a wave's candidate groups in one tile (of 128) past which it tightens first
 constexpr uint32_t kEntPen = 0x80000000u;    // buffer entry flags (ids < 2^22)
 constexpr uint32_t kEntAllowed = 0x40000000u;
 constexpr uint32_t kEntId = 0x003FFFFFu;
@@ -79,7 +79,6 @@ __device__ __forceinline__ uint32_t* lds_bitmap() { return reinterpret_cast<uint
 __device__ __forceinline__ uint32_t* lds_hkey() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashKey); }
 __device__ __forceinline__ uint32_t* lds_hcnt() { return reinterpret_cast<uint32_t*>(lds_base() + kOffHashCnt); }
 __device__ __forceinline__ uint32_t* lds_shist() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSHist); }
-__device__ __forceinline__ uint32_t* lds_seg_pub() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg); }
 // One word per wave, written only by that wave: no other wave's write can
 // race its initialisation, so the stream needs no barrier for it.
 __device__ __forceinline__ uint32_t* lds_nan_wave() { return reinterpret_cast<uint32_t*>(lds_base() + kOffNanW); }
@@ -88,9 +87,6 @@ __device__ __forceinline__ uint32_t* lds_nan_wave() { return reinterpret_cast<ui
 __device__ __forceinline__ bool row_has_nan() {
     const uint32_t lane = lane_id();
     return wave_ballot(lane < kBlock / kWave && lds_nan_wave()[lane] != 0u) != 0u;
-}
-__device__ __forceinline__ uint32_t* lds_seg_done() {
-    return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg + (kBlock / kWave) * 4);
 }
 
 // The running thresholds are canon keys in LDS (misc[M_THR + g]), raised
@@ -442,35 +438,80 @@ __device__ __forceinline__ void raise_from(uint32_t hh, uint32_t need0, uint32_t
     }
 }
 
-// After the first tile each wave appends its candidates to a segment of its
-// own (segment w starts at seg0 + w * seg_cap) and publishes the segment's
-// fill.  The wave that raises the thresholds first counts what was published
-// since the last count: it claims each segment's new range with atomicMax on
-// the counted fill, so two raising waves never count an entry twice.
-__device__ __forceinline__ void count_published(const SHist& h, uint32_t seg0, uint32_t seg_cap) {
-    constexpr uint32_t NW = kBlock / kWave;
+// ---- candidate groups of the stream ----------------------------------------------
+// From the first tile on, the stream keeps its candidates as groups: the four
+// values of one float4 load (an aligned group of ids) whenever any of them is
+// at or above a threshold, with a tag: the group's first id | its allowed
+// nibble << 24.  One compare of the group's maximum decides a group, so the
+// stream spends about one instruction per element on candidates; which of a
+// group's ids are candidates, and which of them are penalized, is sorted out
+// only where groups are counted for a raise and where the stream is closed
+// up.  A group is kept on its raw values: a penalized id may pass on its raw
+// value and is filtered later.  The group area lies past the first tile's
+// distance histograms and ends before the penalized list.
+//
+// Waves take room for a tile's groups from one bump counter (an LDS atomic
+// per wave and tile) and then publish the range in a log slot of its own, so
+// the room goes to whichever waves need it.  A raise counts the log's
+// published ranges in log order, up to the first slot not yet published.
+constexpr uint32_t kG4Base = kOffHist + 4096;               // float4[kG4Cap] values, u32[kG4Cap] tags, u32[kG4Log] log
+constexpr uint32_t kG4Cap = 3264;
+constexpr uint32_t kG4Log = 1024;                           // reservations per row (16 waves x 64 tiles)
+constexpr uint32_t kG4Tag = kG4Base + kG4Cap * 16;
+constexpr uint32_t kG4LogOff = kG4Tag + kG4Cap * 4;
+static_assert(kG4Base % 16 == 0 && kG4LogOff + kG4Log * 4 <= kOffPen,
+              "group area between the histograms and the penalized list");
+constexpr uint32_t kG4Nib = 24;                             // tag: allowed nibble's shift
+constexpr uint32_t kG4Raise = 128;                          // groups between two raises on demand
+constexpr uint32_t kG4Held = (kG4Cap + kBlock - 1) / kBlock;  // groups per thread at the close-up
+__device__ __forceinline__ float4* lds_g4val() { return reinterpret_cast<float4*>(lds_base() + kG4Base); }
+__device__ __forceinline__ uint32_t* lds_g4tag() { return reinterpret_cast<uint32_t*>(lds_base() + kG4Tag); }
+// log slot: the range's first group | its group count << 16 (0: not published)
+__device__ __forceinline__ uint32_t* lds_g4log() { return reinterpret_cast<uint32_t*>(lds_base() + kG4LogOff); }
+// counters, in the stream's scalar words: G_FILL holds the groups reserved
+// (bits 0-15) and the log slots reserved (bits 16-31), so that one atomicAdd
+// reserves a slot and its range and the slots' ranges follow each other in
+// slot order; G_LOGDONE is the first slot not yet counted by a raise
+enum : uint32_t { G_FILL = 0, G_LOGDONE = 2 };
+constexpr uint32_t kG4SlotOne = 1u << 16;
+__device__ __forceinline__ uint32_t* lds_gctr() { return reinterpret_cast<uint32_t*>(lds_base() + kOffSeg); }
+__device__ __forceinline__ float g4_at(const float4& x, uint32_t c) {
+    return c == 0u ? x.x : (c == 1u ? x.y : (c == 2u ? x.z : x.w));
+}
+
+// Counts the groups published since the last count (one wave): the log slots
+// from the counted mark up to the first one not yet published (at most 64)
+// are claimed with atomicMax on the mark, so two raising waves never count a
+// slot twice.  Their ranges follow each other in the area, so the wave's
+// lanes take the claimed groups in turn; each group's ids inside the row that
+// are not penalized (the row's history bitmap, when it has one) are counted
+// by their values.
+__device__ __forceinline__ void count_published_g(const SHist& h, uint32_t n, bool pen_lookup) {
     const uint32_t lane = lane_id();
-    uint32_t from = 0, to = 0;
-    if (lane < NW) {
-        to = lds_load_acquire(&lds_seg_pub()[lane]);
-        from = atomicMax(&lds_seg_done()[lane], to);
-        from = min(from, to);  // a raise that got further: nothing left here
-    }
-    // all segments at once: lane l counts entries l / NW, l / NW + 4, ... of
-    // segment l % NW (the ranges reach the other lanes in one permute)
-    static_assert(kWave == 4 * NW, "four lanes per segment");
-    const uint32_t w = lane % NW, sub = lane / NW;
-    const uint32_t f = static_cast<uint32_t>(__shfl(static_cast<int>(from), static_cast<int>(w), kWave));
-    const uint32_t e = static_cast<uint32_t>(__shfl(static_cast<int>(to), static_cast<int>(w), kWave));
-    if (f + sub < e) {
-        // every reading lane acquires the fill itself (it is at least e:
-        // fills only grow), so its reads are ordered after the writes
-        (void)lds_load_acquire(&lds_seg_pub()[w]);
-        const uint2* seg = lds_buf() + seg0 + w * seg_cap;
-        for (uint32_t i = f + sub; i < e; i += kWave / NW) {
-            const uint2 en = seg[i];
-            if (!(en.y & kEntPen)) count_kept(__uint_as_float(en.x), (en.y & kEntAllowed) != 0u, h);
-        }
+    uint32_t* ctr = lds_gctr();
+    const uint32_t d = lds_load_relaxed(&ctr[G_LOGDONE]);
+    const uint32_t nlog = min(lds_load_relaxed(&ctr[G_FILL]) >> 16, kG4Log);
+    const uint32_t i = d + lane;
+    const uint32_t ent = i < nlog ? lds_load_acquire(&lds_g4log()[i]) : 0u;
+    const uint64_t open = wave_ballot(ent == 0u);
+    const uint32_t k = open ? static_cast<uint32_t>(__builtin_ctzll(open)) : kWave;  // published slots d .. d+k-1
+    if (k == 0u) return;
+    uint32_t from = 0;
+    if (lane == 0) from = atomicMax(&ctr[G_LOGDONE], d + k);
+    from = wave_read(from, 0);
+    if (from >= d + k) return;  // another raise counted them
+    const uint32_t e0 = wave_read(ent, from - d), e1 = wave_read(ent, k - 1u);
+    const uint32_t g_from = e0 & 0xFFFFu, g_to = (e1 & 0xFFFFu) + (e1 >> 16);
+    const float4* gv = lds_g4val();
+    const uint32_t* gt = lds_g4tag();
+    for (uint32_t g = g_from + lane; g < g_to; g += kWave) {
+        const float4 x = gv[g];
+        const uint32_t tag = gt[g];
+        const uint32_t id0 = tag & kEntId;
+        const uint32_t pb = pen_lookup ? lds_bitmap()[id0 >> 5] >> (id0 & 31u) : 0u;
+#pragma unroll
+        for (uint32_t c = 0; c < 4u; c++)
+            if (id0 + c < n && !((pb >> c) & 1u)) count_kept(g4_at(x, c), (tag >> (kG4Nib + c)) & 1u, h);
     }
 }
 
@@ -693,12 +734,6 @@ __device__ __forceinline__ uint32_t emit_mask(float tAR, float tL, const float (
     return emit & elig;
 }
 
-// Buffer entry of element e of this thread's tile.
-__device__ __forceinline__ uint2 make_entry(float y, uint32_t id, uint32_t pen_bits, uint32_t al_bits, int e) {
-    return make_uint2(__float_as_uint(y), id | (((pen_bits >> e) & 1u) ? kEntPen : 0u) |
-                                              (((al_bits >> e) & 1u) ? kEntAllowed : 0u));
-}
-
 // Per-tile work of every thread before the candidates: logsumexp partials of
 // the raw logits and the flags.  Ids past the row hold -inf and add 0; a
 // tile whose terms grow past 2^100 moves the reference to its own maximum.  Penalized ids are not
@@ -794,51 +829,6 @@ __device__ __forceinline__ uint32_t geo_shift(uint32_t base, uint32_t top) {
     const uint32_t span = top > base ? top - base : 0u;
     const int bits = 32 - __clz(static_cast<int>(span));
     return bits > 8 ? static_cast<uint32_t>(bits - 8) : 0u;
-}
-
-// Stream candidate test of element e after the first tile: at or above the
-// all / raw threshold, or allowed and at or above the allowed threshold (only
-// compared when it is the lower one: kL), and inside the row (only checked in
-// the row's last tile: kTail).  Penalized ids pass on their raw value here;
-// their entries carry kEntPen and are dropped when the segments are closed
-// up (their penalized values join at the end).
-template <bool kL, bool kTail>
-__device__ __forceinline__ bool stream_cand(const float (&v)[kVec][4], int e, const TileFlags& fl, float tAR,
-                                            float tL) {
-    const float y = v[e >> 2][e & 3];
-    bool k = y >= tAR;
-    if (kL) k = static_cast<bool>(k | (static_cast<bool>((fl.al >> e) & 1u) & (y >= tL)));
-    if (kTail) k = static_cast<bool>(k & static_cast<bool>((fl.valid >> e) & 1u));
-    return k;
-}
-
-// Candidates of this wave in one tile (uniform).
-template <bool kL, bool kTail>
-__device__ __forceinline__ uint32_t stream_count(const float (&v)[kVec][4], const TileFlags& fl, float tAR, float tL) {
-    uint32_t tot = 0;
-#pragma unroll
-    for (int e = 0; e < kVec * 4; e++)
-        tot += static_cast<uint32_t>(__popcll(wave_ballot(stream_cand<kL, kTail>(v, e, fl, tAR, tL))));
-    return tot;
-}
-
-// Writes this wave's candidates of one tile from buffer index pos on, in
-// element-slot order (a slot's lanes in lane order, placed by their ballot).
-template <bool kL, bool kTail>
-__device__ __forceinline__ void stream_write(const float (&v)[kVec][4], const TileFlags& fl, float tAR, float tL,
-                                             uint32_t pos, uint32_t tb) {
-    const uint32_t tid = threadIdx.x;
-    uint2* buf = lds_buf();
-#pragma unroll
-    for (int e = 0; e < kVec * 4; e++) {
-        const bool k = stream_cand<kL, kTail>(v, e, fl, tAR, tL);
-        const uint64_t b = wave_ballot(k);
-        if (b == 0) continue;
-        if (k)
-            buf[pos + lanes_below(b)] =
-                make_entry(v[e >> 2][e & 3], tb + 4u * ((e >> 2) * kBlock + tid) + (e & 3), fl.pen, fl.al, e);
-        pos += static_cast<uint32_t>(__popcll(b));
-    }
 }
 
 // After the streaming pass: logsumexp and allowed count, then the pick (or
@@ -1121,7 +1111,6 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, const Fin& f_in,
 // sorts and applies the reference's arithmetic.  Within the wave, lanes talk
 // through LDS between wave barriers (the wave runs in lockstep; the barrier
 // keeps the compiler from reordering across it).
-constexpr uint32_t kWaveList = 64;                  // longest ranked list the wave finish takes
 constexpr uint32_t kListCap = 1024;                 // entries of each filtered list (the wave finish takes no more)
 __device__ __forceinline__ uint2* lds_swin() { return reinterpret_cast<uint2*>(lds_base()); }  // region A
 __device__ __forceinline__ uint64_t* lds_sraw() { return reinterpret_cast<uint64_t*>(lds_base() + kListCap * 8); }
@@ -1376,6 +1365,50 @@ __device__ __forceinline__ uint64_t wave_sort_rank(uint64_t v, uint32_t n) {
     const uint64_t r = lane < n ? t[lane] : ~0ull;
     __builtin_amdgcn_wave_barrier();
     return r;
+}
+
+// Rank sort of up to kRankMax distinct keys by one wave: the keys in
+// lds_rkeys()[0..n), padded with ~0 keys to a multiple of 8; each lane takes
+// K = ceil(n / 64) of them, counts for each the keys below it, eight keys per
+// step with loads every lane makes at the same address, and writes it at its
+// rank in lds_rsorted().  n / 8 steps of 8K compares per lane.
+constexpr uint32_t kRankMax = 256;
+__device__ __forceinline__ uint64_t* lds_rkeys() { return reinterpret_cast<uint64_t*>(lds_base() + kOffHist + 4096); }
+__device__ __forceinline__ uint64_t* lds_rsorted() { return lds_rkeys() + kRankMax + 8; }
+static_assert(4096 + (2 * kRankMax + 8) * 8 <= kBins * 12, "rank sort scratch fits the histogram region");
+template <uint32_t K>
+__device__ __forceinline__ void wave_rank_sort_k(uint32_t n) {
+    const uint32_t lane = lane_id();
+    const uint64_t* t = lds_rkeys();
+    uint64_t v[K];
+    uint32_t rk[K];
+#pragma unroll
+    for (uint32_t k = 0; k < K; k++) {
+        const uint32_t i = k * kWave + lane;
+        v[k] = i < n ? t[i] : ~0ull;
+        rk[k] = 0;
+    }
+    for (uint32_t j = 0; j < n; j += 8) {
+        uint64_t a[8];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; q++) a[q] = t[j + q];
+#pragma unroll
+        for (uint32_t q = 0; q < 8; q++)
+#pragma unroll
+            for (uint32_t k = 0; k < K; k++) rk[k] += a[q] < v[k] ? 1u : 0u;
+    }
+    // the wave's reads above complete before its writes below (LDS operations
+    // of one wave run in order)
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (uint32_t k = 0; k < K; k++)
+        if (k * kWave + lane < n) lds_rsorted()[rk[k]] = v[k];
+    __builtin_amdgcn_wave_barrier();
+}
+__device__ __forceinline__ void wave_rank_sort(uint32_t n) {
+    if (n <= kWave) wave_rank_sort_k<1>(n);
+    else if (n <= 2 * kWave) wave_rank_sort_k<2>(n);
+    else wave_rank_sort_k<4>(n);
 }
 
 // The reference's arithmetic on a ranked list held one entry per lane (lane
@@ -1636,9 +1669,33 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
         // threshold is listed, so the count is the rank of ta in the row
         // whenever it is <= W), and the window boundary is not needed.
         uint64_t ta = ~0ull;
-        bool fast = false;
+        bool fast = false, sorted = false;
         if (m.constrained) {
-            ta = wave_kth_reg(nwin, m.want, allowed_c);
+            // the window list's allowed keys, ranked against each other when
+            // at most kRankMax: the want-th is then read off, and the kept list
+            // is the sorted prefix
+            uint32_t nal = 0;
+            uint64_t* rk = lds_rkeys();
+#pragma unroll
+            for (uint32_t r = 0; r < kWaveRegs; r++) {
+                if (r * kWave >= nwin) break;
+                uint64_t c = 0;
+                const bool in = r * kWave + lane < nwin && allowed_c(r, &c);
+                const uint64_t b = wave_ballot(in);
+                const uint32_t at = nal + lanes_below(b);
+                if (in && at < kRankMax) rk[at] = c;
+                nal += static_cast<uint32_t>(__popcll(b));
+            }
+            if (nal <= kRankMax && nal >= m.want) {
+                if (lane < 8u) rk[nal + lane] = ~0ull;  // the pad to a multiple of 8
+                __builtin_amdgcn_wave_barrier();
+                wave_rank_sort(nal);
+                ta = lds_rsorted()[m.want - 1u];
+                sorted = true;
+            } else {
+                __builtin_amdgcn_wave_barrier();
+                ta = wave_kth_reg(nwin, m.want, allowed_c);
+            }
             if (ta != ~0ull) {
                 uint32_t rank = 0;
 #pragma unroll
@@ -1651,7 +1708,9 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             }
         }
         uint32_t g;
-        if (fast) {
+        if (fast && sorted) {
+            g = m.want;  // lds_rsorted()[0..want): the kept list, in order
+        } else if (fast) {
             g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return allowed_c(r, c) && *c <= ta; });
         } else if (!m.constrained) {
             // the window boundary: the W-th best by IEEE order (top_n, sampler.rs:192-194)
@@ -1688,7 +1747,8 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             }
         }
         const uint32_t len = min(g, m.want);
-        const uint64_t mine = wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
+        const uint64_t mine = (fast && sorted) ? (lane < len ? lds_rsorted()[lane] : ~0ull)
+                                               : wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
         if (len == 0) {
             pk.token = 0xFFFFFFFFu;  // nothing to rank (e.g. NaN logits): flagged below
         } else {
@@ -1817,8 +1877,42 @@ __device__ __noinline__ void finish_nan_call() {
     finish_nan(a, f, nlp);
 }
 
-template <bool kVecLoads>
-__global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
+// A penalty that can only lower a value: repetition penalty >= 1 (finite),
+// presence and frequency penalties >= 0 (finite) (sampler.rs:165-175 and the
+// extension).
+__device__ __forceinline__ bool lowers_only(const tsm_row_params& P) {
+    return P.repetition_penalty >= 1.0f && P.repetition_penalty <= 3.4e38f && P.frequency_penalty >= 0.0f &&
+           P.frequency_penalty <= 3.4e38f && P.presence_penalty >= 0.0f && P.presence_penalty <= 3.4e38f;
+}
+
+// The general finish of a row the lean kernel could not finish on one wave
+// (candidates past its buffers): its arguments come through LDS, so the call
+// passes only the per-thread partials in registers and adds nothing to the
+// lean kernel's register use.
+struct RowCall {
+    SampleArgs a;
+    Fin f;
+    Targets tg0;
+    uint32_t nlp, bufn;
+};
+static_assert(sizeof(RowCall) <= kBins * 12, "RowCall fits the histogram area");
+__device__ __forceinline__ RowCall* row_call() { return reinterpret_cast<RowCall*>(lds_base() + kOffHist); }
+__device__ __noinline__ void finish_row_call(float lref, double lsum, uint32_t nallow) {
+    const SampleArgs a = row_call()->a;
+    const Fin f = row_call()->f;
+    const Targets tg0 = row_call()->tg0;
+    const uint32_t nlp = row_call()->nlp, bufn = row_call()->bufn;
+    TSM_LDS_SYNC();  // read by every thread before the finish reuses the area
+    finish_row(a, f, tg0, nlp, lref, lsum, nallow, bufn);
+}
+
+// One row of a sampling step.  kLean: the lean kernel, which takes only the
+// rows of lean_takes (and finishes a row it cannot finish on one wave, a NaN
+// logit or candidates past its buffers, through out-of-line calls);
+// otherwise the general kernel, which leaves those rows to the lean kernel
+// when it runs (a.skip_lean).
+template <bool kVecLoads, bool kLean>
+__device__ __forceinline__ void sample_row(const SampleArgs& a) {
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const uint32_t n = a.usable;
     // first the loads that depend on nothing: the row's history offsets,
@@ -1847,6 +1941,23 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         __uint_as_float(const_as(a.uniforms ? reinterpret_cast<const uint32_t*>(a.uniforms) + row : kZeroWords)[0]);
     const uint32_t* mp = a.mask ? a.mask + static_cast<size_t>(row) * a.mask_stride
                                 : reinterpret_cast<const uint32_t*>(rowp0);
+    // which kernel takes the row, decided before any tile is requested
+    if (kLean || a.skip_lean) {
+        const uint32_t hl = h1 > h0 ? h1 - h0 : 0u;
+        const RowMode m0 = row_mode(P, n, hl, a.mask != nullptr && !a.distribution);
+        if (a.skip_split && split::takes_row(m0, hl)) return;  // sampled by split_kernel
+        const bool lean = lean_takes(m0, P, hl, n, a.distribution != 0u);
+        if (!kLean && lean) return;  // sampled by the lean kernel
+        if (kLean && !lean) {
+            // sampled by the general kernel; without it (the batch said it
+            // holds no such row) the row is reported instead
+            if (!a.general && tid == 0) {
+                a.out_token[row] = 0;
+                atomicOr(a.status, TSM_STATUS_ROW_KIND);
+            }
+            return;
+        }
+    }
     load_logits<kVecLoads>(rowp0, 0, n, v);
     load_mask(mp, 0, n, mw);
     load_logits<kVecLoads>(rowp0, kTile, n, vB);
@@ -1882,7 +1993,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         nlp = a.top_stride;
     }
     // penalties need the history lookup; without it the stream keeps no candidates
-    const bool fast_hist = !m.penal || (hlen <= kHistFast && n <= 32 * kBitmapWords);
+    const bool fast_hist = kLean || !m.penal || (hlen <= kHistFast && n <= 32 * kBitmapWords);
     Targets tg;
     tg.need[SK_ALL] = (m.topk && fast_hist) ? m.window : 0u;
     // the raw top-n, and the raw best for the logsumexp / the argmax when nothing is allowed
@@ -1890,9 +2001,18 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     tg.need[SK_ALLOWED] = (m.topk && m.constrained && fast_hist) ? m.want : 0u;
     Targets tg0 = tg;
     if (!fast_hist) tg0.need[SK_RAW] = 0u;
-    const bool tracking = (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
-    const bool pen_lookup = m.penal && fast_hist;  // the stream sees which ids are penalized
-    const bool track_pen = pen_lookup && tracking;  // and lists them with their raw values
+    const bool tracking = kLean || (tg.need[SK_ALL] | tg.need[SK_RAW] | tg.need[SK_ALLOWED]) != 0;
+    const bool pen_lookup = m.penal && fast_hist;  // the row's history bitmap and counts are built
+    // A penalty that can only lower a value (repetition penalty >= 1, finite;
+    // presence and frequency penalties >= 0, finite: sampler.rs:165-175 and
+    // the extension) leaves every penalized value at or below its raw value,
+    // so the stream's groups, kept on raw values, hold every penalized id the
+    // finish can need, and the penalized list is filed from them when the
+    // stream is closed up.  Otherwise the penalized list is gathered up front
+    // from the history table (a penalized value may rise above its raw value).
+    const bool lower_only = kLean || lowers_only(P);
+    const bool track_pen = pen_lookup && tracking && !lower_only;  // the list gathered up front
+    const bool file_pen = pen_lookup && tracking && lower_only;     // the list filed at the close-up
     if (tid == 0) {
         misc[M_BUFN] = 0;
         misc[M_PENN] = 0;
@@ -1902,7 +2022,8 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     }
     if (tracking) {  // first used after the first tile's barriers
         for (uint32_t i = tid; i < 2 * kSBins; i += kBlock) lds_shist()[i] = 0;
-        if (tid < 2 * (kBlock / kWave)) lds_seg_pub()[tid] = 0;  // published and counted fills
+        if (tid < 4) lds_gctr()[tid] = 0;  // group, log and count counters
+        for (uint32_t i = tid; i < kG4Log; i += kBlock) lds_g4log()[i] = 0u;
     }
     // three register sets take the tiles in turn (tile t in set t mod 3):
     // tiles t+1 and t+2 are in flight while tile t is processed, and no set is
@@ -1940,9 +2061,6 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     sh.shift[0] = sh.shift[1] = 0;
     bool wave_track = tracking;  // uniform per wave; cleared once the buffer overflows
     const uint32_t wid = tid / kWave, lane = lane_id();
-    // buffer segments: the first tile's entries fill [0, seg0), then each wave
-    // owns seg_cap entries; seg_fill is this wave's fill (uniform in the wave)
-    uint32_t seg0 = 0, seg_cap = 0, seg_fill = 0;
 
     // ---------------- streaming pass ----------------
     if (lane == 0) lds_nan_wave()[wid] = 0u;
@@ -1964,101 +2082,96 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     load_tile<kVecLoads>(rowp, mp, 2 * kTile, n, vC, mwC);  // prefetch
     {
         // first tile: block-wide, so the thresholds can start from the tile's
-        // own group-max bounds
+        // own group-max bounds; its groups fill [0, seg0) of the group area
         const TileFlags fl = tile_prep(v, mw, 0, n, m.logprobs, pen_lookup, m.constrained, lse, nallow);
         if (tracking) {
+            uint32_t k[3] = {0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < kVec * 4; e++) {
+                if (!((fl.elig >> e) & 1u)) continue;
+                const float y = v[e >> 2][e & 3];
+                k[SK_ALL] = max(k[SK_ALL], canon_key(y));
+                if ((fl.al >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
+            }
+            k[SK_RAW] = k[SK_ALL];  // bounds from the non-penalized ids
+            uint32_t top[3], key[3], low;
+            tile_bounds(tg, k[0], k[1], k[2], key, top, &low);
             float th[3];
 #pragma unroll
-            for (int g = 0; g < 3; g++) th[g] = thr_float(tg.need[g] ? kKeyNegInf : kKeyUntracked);
-            uint32_t emit = 0, total = 0, pos0 = 0;
-            bool bound = ntiles > 1;
-            if (!bound) {
-                emit = emit_mask(fminf(th[SK_ALL], th[SK_RAW]), th[SK_ALLOWED], v, fl.elig, fl.al);
-                pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
-                bound = total > kBufCap;
-            }
-            if (bound) {
-                uint32_t k[3] = {0u, 0u, 0u};
+            for (int g = 0; g < 3; g++) th[g] = thr_float(key[g]);
+            // histogram geometry: H[0] from the all / raw bounds; H[1] from
+            // the allowed bound, or H[0]'s when the first tile gave none
+            uint32_t b0 = kKeyUntracked, t0 = 0;
 #pragma unroll
-                for (int e = 0; e < kVec * 4; e++) {
-                    if (!((fl.elig >> e) & 1u)) continue;
-                    const float y = v[e >> 2][e & 3];
-                    k[SK_ALL] = max(k[SK_ALL], canon_key(y));
-                    if ((fl.al >> e) & 1u) k[SK_ALLOWED] = max(k[SK_ALLOWED], total_key(y));
+            for (int g = 0; g < 2; g++)
+                if (tg.need[g]) {
+                    b0 = min(b0, key[g]);
+                    t0 = max(t0, top[g]);
                 }
-                k[SK_RAW] = k[SK_ALL];  // the stream's candidates are the non-penalized ids
-                uint32_t top[3], key[3], low;
-                tile_bounds(tg, k[0], k[1], k[2], key, top, &low);
-#pragma unroll
-                for (int g = 0; g < 3; g++) th[g] = thr_float(key[g]);
-                // histogram geometry: H[0] from the all / raw bounds; H[1] from
-                // the allowed bound, or H[0]'s when the first tile gave none
-                uint32_t b0 = kKeyUntracked, t0 = 0;
-#pragma unroll
-                for (int g = 0; g < 2; g++)
-                    if (tg.need[g]) {
-                        b0 = min(b0, key[g]);
-                        t0 = max(t0, top[g]);
-                    }
-                sh.base[0] = b0;
-                sh.shift[0] = geo_shift(b0, t0);
-                if (tg.need[SK_ALLOWED] && key[SK_ALLOWED] > kKeyNegInf) {
-                    sh.base[1] = key[SK_ALLOWED];
-                    sh.shift[1] = geo_shift(key[SK_ALLOWED], top[SK_ALLOWED]);
-                } else if (tg.need[SK_ALLOWED] && b0 > low && t0 > b0) {
-                    // too few allowed ids in the first tile to bound them: the
-                    // allowed histogram reaches three spans of the window
-                    // histogram further down (not below the tile's lowest
-                    // group maximum), so allowed candidates below the other
-                    // thresholds are still counted
-                    const uint64_t ext = min(3ull * (t0 - b0), static_cast<uint64_t>(b0 - low));
-                    sh.base[1] = b0 - static_cast<uint32_t>(ext);
-                    sh.shift[1] = geo_shift(sh.base[1], t0);
-                } else {
-                    sh.base[1] = sh.base[0];
-                    sh.shift[1] = sh.shift[0];
-                }
-                emit = emit_mask(fminf(th[SK_ALL], th[SK_RAW]), th[SK_ALLOWED], v, fl.elig, fl.al);
-                pos0 = block_excl_scan<kBlock>(__popc(emit), lds_tmp(), &total);
+            sh.base[0] = b0;
+            sh.shift[0] = geo_shift(b0, t0);
+            if (tg.need[SK_ALLOWED] && key[SK_ALLOWED] > kKeyNegInf) {
+                sh.base[1] = key[SK_ALLOWED];
+                sh.shift[1] = geo_shift(key[SK_ALLOWED], top[SK_ALLOWED]);
+            } else if (tg.need[SK_ALLOWED] && b0 > low && t0 > b0) {
+                // too few allowed ids in the first tile to bound them: the
+                // allowed histogram reaches three spans of the window
+                // histogram further down (not below the tile's lowest
+                // group maximum), so allowed candidates below the other
+                // thresholds are still counted
+                const uint64_t ext = min(3ull * (t0 - b0), static_cast<uint64_t>(b0 - low));
+                sh.base[1] = b0 - static_cast<uint32_t>(ext);
+                sh.shift[1] = geo_shift(sh.base[1], t0);
+            } else {
+                sh.base[1] = sh.base[0];
+                sh.shift[1] = sh.shift[0];
             }
-            if (total > kBufCap) {  // uniform: stop tracking, the finish re-reads
-                if (tid == 0) misc[M_OVF] = 1u;
-                wave_track = false;
-                emit = 0;
-                total = 0;
+            // a group is kept when any of its ids in the row passes on its raw
+            // value (penalized ids too); the non-penalized ones that pass are
+            // counted for the raises
+            const float tAR = fminf(th[SK_ALL], th[SK_RAW]), tL = th[SK_ALLOWED];
+            const uint32_t pass = emit_mask(tAR, tL, v, fl.valid, fl.al);
+            uint32_t gpass = 0;
+#pragma unroll
+            for (int j = 0; j < kVec; j++) gpass |= ((pass >> (4 * j)) & 0xFu) ? (1u << j) : 0u;
+            uint32_t total;
+            uint32_t pos = block_excl_scan<kBlock>(__popc(gpass), lds_tmp(), &total);
+            float4* gv = lds_g4val();
+            uint32_t* gt = lds_g4tag();
+#pragma unroll
+            for (int j = 0; j < kVec; j++) {
+                if (!((gpass >> j) & 1u)) continue;
+                gv[pos] = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+                gt[pos] = (4u * (j * kBlock + tid)) | (((fl.al >> (4 * j)) & 0xFu) << kG4Nib);
+                pos++;
             }
-            uint32_t pos = pos0;
+            const uint32_t cnt = pass & fl.elig;
 #pragma unroll
             for (int e = 0; e < kVec * 4; e++)
-                if ((emit >> e) & 1u) {
-                    const float y = v[e >> 2][e & 3];
-                    buf[pos++] = make_entry(y, 4u * ((e >> 2) * kBlock + tid) + (e & 3), 0u, fl.al, e);
-                    if (bound) count_kept(y, (fl.al >> e) & 1u, sh);
-                }
+                if ((cnt >> e) & 1u) count_kept(v[e >> 2][e & 3], (fl.al >> e) & 1u, sh);
             if (track_pen) {
                 // one LDS atomic per wave reserves the wave's places
                 uint64_t b[kSlotsPerThread];
-                uint32_t cnt = 0;
+                uint32_t cntp = 0;
 #pragma unroll
-                for (uint32_t k = 0; k < kSlotsPerThread; k++) {
-                    b[k] = wave_ballot(pen_id[k] != 0xFFFFFFFFu);
-                    cnt += static_cast<uint32_t>(__popcll(b[k]));
+                for (uint32_t q = 0; q < kSlotsPerThread; q++) {
+                    b[q] = wave_ballot(pen_id[q] != 0xFFFFFFFFu);
+                    cntp += static_cast<uint32_t>(__popcll(b[q]));
                 }
                 uint32_t at = 0;
-                if (cnt && lane == 0) at = atomicAdd(&misc[M_PENN], cnt);
+                if (cntp && lane == 0) at = atomicAdd(&misc[M_PENN], cntp);
                 at = wave_uniform(wave_read(at, 0));
 #pragma unroll
-                for (uint32_t k = 0; k < kSlotsPerThread; k++) {
-                    const uint32_t id = pen_id[k];
+                for (uint32_t q = 0; q < kSlotsPerThread; q++) {
+                    const uint32_t id = pen_id[q];
                     if (id != 0xFFFFFFFFu) {
-                        const bool al = m.constrained && ((pen_w[k] >> (id & 31u)) & 1u);
-                        pen[at + lanes_below(b[k])] = make_uint2(__float_as_uint(pen_x[k]), id | (al ? kEntAllowed : 0u));
+                        const bool al = m.constrained && ((pen_w[q] >> (id & 31u)) & 1u);
+                        pen[at + lanes_below(b[q])] = make_uint2(__float_as_uint(pen_x[q]), id | (al ? kEntAllowed : 0u));
                     }
-                    at += static_cast<uint32_t>(__popcll(b[k]));
+                    at += static_cast<uint32_t>(__popcll(b[q]));
                 }
             }
-            seg0 = total;
-            seg_cap = ((kBufCap - total) / (kBlock / kWave)) & ~1u;
+            if (tid == 0) lds_gctr()[G_FILL] = total;  // <= kVec * kBlock groups
             TSM_LDS_SYNC();
         }
     }
@@ -2078,29 +2191,79 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             kR = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]);
             kL = lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)]);
         }
-        const TileFlags fl = tile_prep(v, mw, tb, n, m.logprobs, pen_lookup, m.constrained, lse, nallow);
+        const TileFlags fl = tile_prep(v, mw, tb, n, m.logprobs, false, m.constrained, lse, nallow);
         if (wave_track && wave_uniform(ovf) != 0u) wave_track = false;  // the finish re-reads the row
         if (wave_track) {
-            // no barriers: each wave appends to its own segment and publishes
-            // the segment's fill
+            // no barriers: each wave appends its groups to its own segment and
+            // publishes the segment's fill
             const bool tail = tb + kTile > n;
             float tAR = fminf(thr_float(wave_uniform(kA)), thr_float(wave_uniform(kR)));
             float tL = thr_float(wave_uniform(kL));
             bool use_l = !(tL >= tAR) && tL == tL;  // allowed ids need a compare of their own
-            auto count = [&]() __attribute__((always_inline)) {
-                return use_l ? (tail ? stream_count<true, true>(v, fl, tAR, tL) : stream_count<true, false>(v, fl, tAR, tL))
-                             : (tail ? stream_count<false, true>(v, fl, tAR, tL) : stream_count<false, false>(v, fl, tAR, tL));
+            // group maxima, over every id and over the allowed ids
+            float gm[kVec], ga[kVec];
+#pragma unroll
+            for (int j = 0; j < kVec; j++) {
+                gm[j] = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+                ga[j] = -INFINITY;
+            }
+            auto group_pass = [&](int j) __attribute__((always_inline)) {
+                bool k = gm[j] >= tAR;
+                // (ga is -inf for a group without allowed ids, which a -inf
+                // allowed threshold would pass: the nibble decides that)
+                if (use_l) k = static_cast<bool>(k | (((fl.al >> (4 * j)) & 0xFu) != 0u && ga[j] >= tL));
+                if (tail) k = static_cast<bool>(k & static_cast<bool>((fl.valid >> (4 * j)) & 0xFu));
+                return k;
             };
-            uint32_t tot = count();
+            auto allowed_max = [&]() __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < kVec; j++) {
+                    float a = -INFINITY;
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        if ((fl.al >> (4 * j + c)) & 1u) a = fmaxf(a, v[j][c]);
+                    ga[j] = a;
+                }
+            };
+            if (use_l) allowed_max();
+            uint64_t gb[kVec];
+            uint32_t tot = 0;
+#pragma unroll
+            for (int j = 0; j < kVec; j++) {
+                gb[j] = wave_ballot(group_pass(j));
+                tot += static_cast<uint32_t>(__popcll(gb[j]));
+            }
+            auto reload = [&]() __attribute__((always_inline)) {
+                tAR = fminf(thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)]))),
+                            thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]))));
+                tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
+                const bool was_l = use_l;
+                use_l = !(tL >= tAR) && tL == tL;
+                if (use_l && !was_l) allowed_max();
+                tot = 0;
+#pragma unroll
+                for (int j = 0; j < kVec; j++) {
+                    gb[j] = wave_ballot(group_pass(j));
+                    tot += static_cast<uint32_t>(__popcll(gb[j]));
+                }
+            };
             if (tot > kBigEmit) {
-                // far more candidates than a tile should bring (a target the
-                // first tile could not bound, or a dense stretch of the row):
-                // raise the thresholds from this wave's own lane maxima, then
-                // keep what still passes
+                // far more groups than a tile should bring (a target the first
+                // tile could not bound, or a dense stretch of the row): raise
+                // the thresholds from this wave's own lane maxima over its ids
+                // that are not penalized, then keep what still passes
+                uint32_t pb = 0;
+                if (pen_lookup) {
+#pragma unroll
+                    for (int j = 0; j < kVec; j++) {
+                        const uint32_t id0 = tb + 4u * (j * kBlock + tid);
+                        pb |= ((lds_bitmap()[min(id0, n - 1u) >> 5] >> (id0 & 31u)) & 0xFu) << (4 * j);
+                    }
+                }
                 uint32_t lmA = 0, lmL = 0;
 #pragma unroll
                 for (int e = 0; e < kVec * 4; e++)
-                    if ((fl.elig >> e) & 1u) {
+                    if (((fl.valid & ~pb) >> e) & 1u) {
                         const uint32_t ck = canon_key(v[e >> 2][e & 3]);
                         lmA = max(lmA, ck);
                         if ((fl.al >> e) & 1u) lmL = max(lmL, ck);
@@ -2112,48 +2275,58 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
                     const uint32_t kb = wave_lane_bound(g == SK_ALLOWED ? lmL : lmA, need);
                     if (kb != 0u && lane == 0) atomicMax(&misc[M_THR + g], kb);
                 }
-                tAR = fminf(thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)]))),
-                            thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]))));
-                tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
-                use_l = !(tL >= tAR) && tL == tL;
-                tot = count();
+                reload();
             }
             if (tot) {
-                if (seg_fill + tot > seg_cap) {
-                    // the segment cannot take the tile's candidates: raise the
+                uint32_t* ctr = lds_gctr();
+                if ((wave_uniform(lds_load_relaxed(&ctr[G_FILL])) & 0xFFFFu) + tot > kG4Cap) {
+                    // the area cannot take the tile's groups: raise the
                     // thresholds from everything published so far (any wave
                     // may raise), then count again before giving up
-                    count_published(sh, seg0, seg_cap);
+                    count_published_g(sh, n, pen_lookup);
                     raise_thresholds(tg, sh);
-                    tAR = fminf(thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALL)]))),
-                                thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_RAW)]))));
-                    tL = thr_float(wave_uniform(lds_load_relaxed(&misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)])));
-                    use_l = !(tL >= tAR) && tL == tL;
-                    tot = count();
+                    reload();
                 }
-                if (seg_fill + tot <= seg_cap) {
-                    const uint32_t pos = seg0 + wid * seg_cap + seg_fill;
-                    if (use_l) {
-                        if (tail) stream_write<true, true>(v, fl, tAR, tL, pos, tb);
-                        else stream_write<true, false>(v, fl, tAR, tL, pos, tb);
-                    } else {
-                        if (tail) stream_write<false, true>(v, fl, tAR, tL, pos, tb);
-                        else stream_write<false, false>(v, fl, tAR, tL, pos, tb);
+                uint32_t r = 0;
+                if (tot && lane == 0) r = atomicAdd(&ctr[G_FILL], tot | kG4SlotOne);
+                r = wave_read(r, 0);
+                const uint32_t at0 = r & 0xFFFFu, slot = r >> 16;
+                if (!tot) {
+                } else if (at0 + tot <= kG4Cap && slot < kG4Log) {
+                    uint32_t pos = at0;
+                    float4* gv = lds_g4val();
+                    uint32_t* gt = lds_g4tag();
+#pragma unroll
+                    for (int j = 0; j < kVec; j++) {
+                        if (gb[j] == 0) continue;
+                        if ((gb[j] >> lane) & 1u) {
+                            const uint32_t at = pos + lanes_below(gb[j]);
+                            gv[at] = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+                            gt[at] = (tb + 4u * (j * kBlock + tid)) | (((fl.al >> (4 * j)) & 0xFu) << kG4Nib);
+                        }
+                        pos += static_cast<uint32_t>(__popcll(gb[j]));
                     }
-                    // the fill each lane publishes covers every lane's entries:
-                    // all lanes' writes come before any lane's publish
+                    // every lane releases its own writes with the publish
+                    // (read-modify-writes of one value: one release sequence)
                     __builtin_amdgcn_wave_barrier();
-                    seg_fill += tot;
-                    lds_publish_max(&lds_seg_pub()[wid], seg_fill);
+                    lds_publish_max(&lds_g4log()[slot], at0 | (tot << 16));
+                    // the wave whose groups cross a multiple of kG4Raise in
+                    // the area raises the thresholds at once: the raises keep
+                    // up with the groups however fast they come
+                    if ((at0 + tot) / kG4Raise != at0 / kG4Raise) {
+                        count_published_g(sh, n, pen_lookup);
+                        raise_thresholds(tg, sh);
+                    }
                 } else {
+                    // no room left (the row is re-read by the finish)
                     if (lane == 0) atomicOr(&misc[M_OVF], 1u);
                     wave_track = false;
                 }
             }
-            // one wave counts what was published and raises the thresholds:
-            // every tile at first, every second tile later on
-            if (wave_track && wid == (t & (kBlock / kWave - 1)) && (t < 8 || (t & 1u) == 0)) {
-                count_published(sh, seg0, seg_cap);
+            // one wave counts what was published and raises the thresholds
+            // on every tile
+            if (wave_track && wid == (t & (kBlock / kWave - 1))) {
+                count_published_g(sh, n, pen_lookup);
                 raise_thresholds(tg, sh);
             }
         }
@@ -2175,45 +2348,101 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     if (tracking) {
         // the stream's final state, read by every thread before anything below
         // changes it (the decisions taken from it must be uniform)
-        const uint32_t ovf0 = misc[M_OVF], penn0 = misc[M_PENN];
+        const uint32_t ovf0 = misc[M_OVF], penn0 = file_pen ? 0u : misc[M_PENN];
         const float tA = thr_float(misc[M_THR + static_cast<uint32_t>(SK_ALL)]);
+        const float tR = thr_float(misc[M_THR + static_cast<uint32_t>(SK_RAW)]);
         const float tL = thr_float(misc[M_THR + static_cast<uint32_t>(SK_ALLOWED)]);
-        // close up the wave segments behind the first tile's entries, dropping
-        // the entries of penalized ids (their penalized values join below):
-        // each wave holds its entries in registers across the barrier, then
-        // writes the kept ones at its place
-        constexpr uint32_t kSegRegs = kBufCap / (kBlock / kWave) / kWave;
-        const uint32_t mine = ovf0 ? 0u : lds_seg_pub()[wid];
-        uint2 held[kSegRegs];
-        bool kept[kSegRegs];
-        uint32_t kept_w = 0;  // uniform
+        const bool need_raw = tg.need[SK_RAW] > 0;
+        const float tAR = fminf(tA, tR);  // a non-penalized entry serves the window and the raw top-n
+        // close-up: every thread takes its share of the groups into
+        // registers, then, after a barrier (the candidate buffer overlaps the group area), writes the
+        // ids that pass the final thresholds as buffer entries: not
+        // penalized on their values; penalized ones, when the penalized list
+        // is filed here, on their penalized values (and into the list on
+        // their raw values, when they can be among the raw top-n).
+        const uint32_t ng = ovf0 ? 0u : min(lds_gctr()[G_FILL] & 0xFFFFu, kG4Cap);  // every reserved group is written
+        constexpr uint32_t kHeld = kG4Held;
+        float4 hv[kHeld];
+        uint32_t ht[kHeld];
 #pragma unroll
-        for (uint32_t k = 0; k < kSegRegs; k++) {
-            const uint32_t i = lane + k * kWave;
-            kept[k] = false;
-            if (i < mine) {
-                held[k] = buf[seg0 + wid * seg_cap + i];
-                kept[k] = !(held[k].y & kEntPen);
+        for (uint32_t q = 0; q < kHeld; q++) {
+            const uint32_t i = tid + q * kBlock;
+            ht[q] = 0xFFFFFFFFu;
+            hv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (i < ng) {
+                hv[q] = lds_g4val()[i];
+                ht[q] = lds_g4tag()[i];
             }
-            kept_w += static_cast<uint32_t>(__popcll(wave_ballot(kept[k])));
         }
-        if (lane == 0) lds_tmp()[wid] = kept_w;
+        if (tid == 0) misc[M_BUFN] = 0u;
         TSM_LDS_SYNC();
-        const uint32_t cw = lane < kBlock / kWave ? lds_tmp()[lane] : 0u;  // one round trip
-        const uint32_t before = row_sum16(lane < wid ? cw : 0u), fill0 = seg0 + row_sum16(cw);
-        uint32_t dst = seg0 + before;
+        // this thread's entries, counted, then written at the wave's places
+        auto pen_bits = [&](uint32_t id0) -> uint32_t {
+            return pen_lookup ? (lds_bitmap()[id0 >> 5] >> (id0 & 31u)) & 0xFu : 0u;
+        };
+        uint32_t nb_mine = 0, np_mine = 0;
 #pragma unroll
-        for (uint32_t k = 0; k < kSegRegs; k++) {
-            const uint64_t b = wave_ballot(kept[k]);
-            if (kept[k]) buf[dst + lanes_below(b)] = held[k];
-            dst += static_cast<uint32_t>(__popcll(b));
+        for (uint32_t q = 0; q < kHeld; q++) {
+            if (ht[q] == 0xFFFFFFFFu) continue;
+            const uint32_t id0 = ht[q] & kEntId, pb = pen_bits(id0);
+#pragma unroll
+            for (uint32_t c = 0; c < 4u; c++) {
+                const uint32_t id = id0 + c;
+                if (id >= n) continue;
+                const float y = g4_at(hv[q], c);
+                const bool al = (ht[q] >> (kG4Nib + c)) & 1u;
+                if (!((pb >> c) & 1u)) {
+                    nb_mine += keep2(y, al, tAR, tL) ? 1u : 0u;
+                } else if (file_pen) {
+                    np_mine += (need_raw && y >= tR) ? 1u : 0u;
+                    nb_mine += keep2(penalize(y, history_count(id), m, P), al, tA, tL) ? 1u : 0u;
+                }
+            }
         }
-        if (tid == 0) misc[M_BUFN] = fill0;
+        const uint32_t wb = wave_incl_scan(nb_mine), wp = wave_incl_scan(np_mine);
+        uint32_t bat = 0, pat = 0;
+        if (lane == kWave - 1) {
+            if (wb) bat = atomicAdd(&misc[M_BUFN], wb);
+            if (wp) pat = atomicAdd(&misc[M_PENN], wp);
+        }
+        bat = wave_read(bat, kWave - 1) + wb - nb_mine;
+        pat = wave_read(pat, kWave - 1) + wp - np_mine;
+        if (nb_mine | np_mine) {
+#pragma unroll
+            for (uint32_t q = 0; q < kHeld; q++) {
+                if (ht[q] == 0xFFFFFFFFu) continue;
+                const uint32_t id0 = ht[q] & kEntId, pb = pen_bits(id0);
+#pragma unroll
+                for (uint32_t c = 0; c < 4u; c++) {
+                    const uint32_t id = id0 + c;
+                    if (id >= n) continue;
+                    const float y = g4_at(hv[q], c);
+                    const bool al = (ht[q] >> (kG4Nib + c)) & 1u;
+                    const uint32_t alf = al ? kEntAllowed : 0u;
+                    if (!((pb >> c) & 1u)) {
+                        if (keep2(y, al, tAR, tL)) {
+                            if (bat < kBufCap) buf[bat] = make_uint2(__float_as_uint(y), id | alf);
+                            bat++;
+                        }
+                    } else if (file_pen) {
+                        if (need_raw && y >= tR) {
+                            if (pat < kPenCap) pen[pat] = make_uint2(__float_as_uint(y), id | alf);
+                            pat++;
+                        }
+                        const float yp = penalize(y, history_count(id), m, P);
+                        if (keep2(yp, al, tA, tL)) {
+                            if (bat < kBufCap) buf[bat] = make_uint2(__float_as_uint(yp), id | kEntPen | alf);
+                            bat++;
+                        }
+                    }
+                }
+            }
+        }
         TSM_LDS_SYNC();
-        // penalized ids join the candidates when their penalized value passes
-        // the final thresholds (every element at or above them is then in the
-        // buffer)
-        if (track_pen && ovf0 == 0u && fill0 <= kBufCap) {
+        // a gathered penalized list: its ids join the candidates when their
+        // penalized value passes the final thresholds (every element at or
+        // above them is then in the buffer)
+        if (track_pen && ovf0 == 0u && misc[M_BUFN] <= kBufCap) {
             const uint32_t penn = min(penn0, kPenCap);
             for (uint32_t i = tid; i < penn; i += kBlock) {
                 const uint2 e = pen[i];
@@ -2228,7 +2457,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
             TSM_LDS_SYNC();
         }
         const uint32_t fill = misc[M_BUFN];
-        if (tid == 0 && (fill > kBufCap || misc[M_OVF] != 0u)) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
+        if (tid == 0 && (fill > kBufCap || misc[M_OVF] != 0u || misc[M_PENN] > kPenCap)) misc[M_FLAGS] |= ROWF_BUF_OVERFLOW;
         bufn = min(fill, kBufCap);
     }
     // a NaN logit (or +inf, whose steps make the sum NaN as well; the serial
@@ -2237,6 +2466,32 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
     // the finish: one wave for the common rows, the whole block otherwise
     TSM_LDS_SYNC();
     const uint32_t flags = misc[M_FLAGS];
+    if constexpr (kLean) {
+        // the single-wave finish; the rare rows it cannot take go through the
+        // out-of-line general finishes (their arguments through LDS)
+        if (row_has_nan()) {
+            if (tid == 0) {
+                nan_call()->a = a;
+                nan_call()->f = f;
+                nan_call()->nlp = nlp;
+            }
+            TSM_LDS_SYNC();
+            finish_nan_call();
+            return;
+        }
+        if (!(flags & (ROWF_BUF_OVERFLOW | ROWF_SLOW_HISTORY)) &&
+            finish_wave(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn))
+            return;
+        if (tid == 0) {
+            row_call()->a = a;
+            row_call()->f = f;
+            row_call()->tg0 = tg0;
+            row_call()->nlp = nlp;
+            row_call()->bufn = bufn;
+        }
+        TSM_LDS_SYNC();
+        finish_row_call(lse.ref, lse.sum, nallow);
+    } else {
     if (m.topk && row_has_nan()) {
         if (tid == 0) {
             nan_call()->a = a;
@@ -2252,24 +2507,55 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
         if (finish_wave(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn)) return;
     }
     finish_row(a, f, tg0, nlp, lse.ref, lse.sum, nallow, bufn);
+    }
+}
+
+// The general kernel: every row kind (re-reads, exact nucleus folds, NaN
+// rows, the block finish).
+template <bool kVecLoads>
+__global__ __launch_bounds__(kBlock) void sample_kernel(SampleArgs a) {
+    sample_row<kVecLoads, false>(a);
+}
+// The lean kernel: the common top-k rows only (lean_takes).  Without the
+// general path inlined, the stream and the single-wave finish keep their
+// state in registers (no scratch).
+template <bool kVecLoads>
+__global__ __launch_bounds__(kBlock) void topk_kernel(SampleArgs a) {
+    sample_row<kVecLoads, true>(a);
 }
 
 template __global__ void sample_kernel<true>(SampleArgs);
 template __global__ void sample_kernel<false>(SampleArgs);
+template __global__ void topk_kernel<true>(SampleArgs);
+template __global__ void topk_kernel<false>(SampleArgs);
 
-void launch_sample(const SampleArgs& a, uint32_t rows, bool vec_loads, hipStream_t stream) {
-    if (vec_loads)
-        hipLaunchKernelGGL(sample_kernel<true>, dim3(rows), dim3(kBlock), kSmem, stream, a);
-    else
-        hipLaunchKernelGGL(sample_kernel<false>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+void launch_sample(const SampleArgs& a_in, uint32_t rows, bool vec_loads, bool lean, bool general,
+                   hipStream_t stream) {
+    SampleArgs a = a_in;
+    a.skip_lean = lean ? 1u : 0u;
+    a.general = general ? 1u : 0u;
+    if (lean) {
+        if (vec_loads)
+            hipLaunchKernelGGL(topk_kernel<true>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+        else
+            hipLaunchKernelGGL(topk_kernel<false>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+    }
+    if (general) {
+        if (vec_loads)
+            hipLaunchKernelGGL(sample_kernel<true>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+        else
+            hipLaunchKernelGGL(sample_kernel<false>, dim3(rows), dim3(kBlock), kSmem, stream, a);
+    }
 }
 
 hipError_t sample_set_smem_attr() {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_kernel<true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmem));
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_kernel<false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmem));
+    const void* ks[4] = {reinterpret_cast<const void*>(&sample_kernel<true>),
+                         reinterpret_cast<const void*>(&sample_kernel<false>),
+                         reinterpret_cast<const void*>(&topk_kernel<true>),
+                         reinterpret_cast<const void*>(&topk_kernel<false>)};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 4 && e == hipSuccess; i++)
+        e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kSmem));
     return e;
 }
 

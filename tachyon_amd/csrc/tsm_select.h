@@ -22,9 +22,6 @@ namespace tsm {
 // history counts.  The histograms, the candidate buffer, the penalized list
 // and the scalars have their own regions.
 constexpr uint32_t kReTile = 8192;         // ids per tile of a re-read pass
-constexpr uint32_t kBitmapWords = 8192;    // history bitmap: rows of up to 262144 ids
-constexpr uint32_t kHashSlots = 4096;      // history count table (histories up to kHistFast ids)
-constexpr uint32_t kHistFast = kHashSlots / 2;
 constexpr uint32_t kBufCap = 6144;         // candidate buffer entries (y bits, id | flags)
 constexpr uint32_t kPenCap = 2048;         // penalized-id list entries (raw x bits, id)
 constexpr uint32_t kOffBitmap = 0;                              // u32[kBitmapWords]
@@ -43,7 +40,7 @@ constexpr uint32_t kOffMiscD = kOffMisc + 64 * 4;                // f64[32]
 constexpr uint32_t kOffTmp = kOffMiscD + 32 * 8;                 // u32[64] scan scratch
 constexpr uint32_t kSBins = 512;                                 // stream histogram bins per threshold
 constexpr uint32_t kOffSHist = kOffTmp + 64 * 4;                 // 2 x u32[kSBins]
-constexpr uint32_t kOffSeg = kOffSHist + 2 * kSBins * 4;         // per wave: published fill, counted fill
+constexpr uint32_t kOffSeg = kOffSHist + 2 * kSBins * 4;         // stream counters (candidate groups)
 constexpr uint32_t kOffNanW = kOffSeg + 2 * (kBlock / kWave) * 4;  // per wave: met a NaN logit
 constexpr uint32_t kSmem = kOffNanW + (kBlock / kWave) * 4;
 static_assert(kOffGather % 8 == 0 && (kOffHist + kBins * 4) % 8 == 0 && kOffBuf % 8 == 0 && kOffPen % 8 == 0 &&
