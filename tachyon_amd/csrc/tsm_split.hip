@@ -111,12 +111,11 @@ __device__ __forceinline__ float lane_f(float v, uint32_t lane) {
 // ---- memory shared between the workgroups of a row -------------------------------
 // Every word one workgroup writes and another reads (candidates, penalized
 // entries, segment summaries, counters) goes through device-scope atomic
-// loads and stores: each such access is coherent across the chip's L2 caches
-// on its own (global_load/store ... sc1), so no L2 writeback or invalidate
-// (the cost of a device-scope fence) is needed.  A writer waits for all its
-// stores to complete (s_waitcnt 0) before its workgroup arrives at the row's
-// counter; the last arrival's loads are issued after it has read the counter,
-// so they see every completed store.
+// loads and stores, each coherent across the chip's L2 caches on its own
+// (global_load/store ... sc1).  The order between a workgroup's stores and
+// the last arrival's loads comes from the arrival itself: workgroup-scope
+// release and acquire around a barrier, and an agent-scope acquire-release
+// read-modify-write of the row's counter (split_kernel).
 __device__ __forceinline__ void dev_st32(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1603,15 +1602,25 @@ __global__ __launch_bounds__(kSB) void split_kernel(SplitArgs a) {
         for (int q = 0; q < 5; q++) S.pad[q] = 0;
         st_sum(a.w.sums + static_cast<size_t>(row) * a.nseg + seg, S);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
-    TSM_LDS_SYNC();
+    // The handoff to the row's last workgroup, in the memory model's terms:
+    // every thread's stores are released at workgroup scope and meet at the
+    // barrier; thread 0's arrival is an agent-scope acquire-release
+    // read-modify-write, so the stores of every workgroup that arrived before
+    // happen before whatever the last arrival reads after its own arrival
+    // (each of its threads acquires at workgroup scope behind the barrier).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (tid == 0) {
-        const uint64_t prev = dev_add64(&a.w.row_ctr[row], 1ull << kCtrArrShift);
+        const uint64_t prev = __hip_atomic_fetch_add(&a.w.row_ctr[row], uint64_t{1} << kCtrArrShift, __ATOMIC_ACQ_REL,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
         s_misc()[MS_LAST] = ctr_arr(prev) == a.nseg - 1u ? 1u : 0u;
         s_misc()[MS_NSTREAM] = ctr_cand(prev);
         s_misc()[MS_NPEN] = ctr_pen(prev);
     }
-    TSM_LDS_SYNC();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (!s_misc()[MS_LAST]) return;
 
     // ================= finish: the row's last workgroup =================
