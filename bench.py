@@ -114,6 +114,11 @@ def main():
     ap.add_argument("--json-mask", action="store_true",
                     help="time the mask producer (tsm_json_mask) instead: 256 JsonObject rows over a "
                          "151936-token synthetic vocabulary")
+    ap.add_argument("--mask-mode", default="direct", choices=["direct", "dedupe", "cached", "decode"],
+                    help="with --json-mask: direct = tsm_json_mask on every row; dedupe = a mask set keeping "
+                         "nothing (each distinct state of a step evaluated once); cached = a mask set keeping "
+                         "1024 states, the same rows every step; decode = a mask set keeping 1024 states, "
+                         "each row advancing through its own document by one 4-byte token per step")
     ap.add_argument("--lm-head", action="store_true",
                     help="time the logits producer (tsm_lm_head) instead: 256 rows, dim 4096, vocab 151936, "
                          "bf16 weights")
@@ -275,27 +280,66 @@ def bench_json_mask(args):
     from tachyon_amd import workloads as wl
     from tachyon_amd.constrain import DeviceVocab, HostVocab, JsonConstraint, json_mask, pack_states
 
+    import numpy as np
+
+    from tachyon_amd.constrain import JsonMaskSet
+
     rows, V = 256, wl.QWEN_VOCAB
     toks, special = wl.json_vocab(V, seed=0x15A0)
     hv = HostVocab.from_tokens(toks, special)
     dv = DeviceVocab(hv)
-    prefixes = wl.json_prefixes(rows, seed=0x15A4)
-    cs = []
-    for p in prefixes:
-        c = JsonConstraint()
-        c.advance(p)
-        cs.append(c)
-    st = torch.from_numpy(pack_states(cs)).cuda()
+    mode = args.mask_mode
+    total = args.warmup + args.steps
+    if mode == "decode":
+        # each row writes its own document, one 4-byte token per step
+        rng = np.random.default_rng(0x15A5)
+        docs = [wl.json_document(rng) for _ in range(rows)]
+        cur = [JsonConstraint() for _ in range(rows)]
+        step_states, step_prefixes = [], []
+        for i in range(total):
+            step_states.append([c.packed() for c in cur])
+            step_prefixes.append([d[:4 * i] for d in docs])
+            for r, c in enumerate(cur):
+                c.advance(docs[r][4 * i:4 * i + 4])
+    else:
+        prefixes = wl.json_prefixes(rows, seed=0x15A4)
+        cs = []
+        for p in prefixes:
+            c = JsonConstraint()
+            c.advance(p)
+            cs.append(c)
+        step_states = [[c.packed() for c in cs]] * total
+        step_prefixes = [prefixes] * total
     stride = (V + 31) // 32
     mask = torch.zeros(rows, stride, dtype=torch.int32, device="cuda")
-    for _ in range(args.warmup):
-        json_mask(dv, st, rows, V, mask, stride)
+    mset = None
+    if mode != "direct":
+        mset = JsonMaskSet(max_rows=rows, capacity=0 if mode == "dedupe" else 1024, usable=V)
+    st_dev = [torch.from_numpy(np.frombuffer(b"".join(ss), np.uint8).copy()).cuda() for ss in step_states[:1]]
+    # the host arrays a caller keeps its states in, built before the timed steps
+    step_arrays = [JsonMaskSet.pack(ss) for ss in step_states] if mode != "direct" else None
+    counts = []
+    host_s = 0.0
+
+    def one(i):
+        nonlocal host_s
+        if mset is None:
+            json_mask(dv, st_dev[0], rows, V, mask, stride)
+            return
+        t0 = time.perf_counter()
+        counts.append(mset.fill(dv, step_arrays[i], mask, stride))
+        host_s += time.perf_counter() - t0
+
+    for i in range(args.warmup):
+        one(i)
     torch.cuda.synchronize()
+    counts.clear()
+    host_s = 0.0
     ea = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     eb = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     for i in range(args.steps):
         ea[i].record()
-        json_mask(dv, st, rows, V, mask, stride)
+        one(args.warmup + i)
         eb[i].record()
     torch.cuda.synchronize()
     us = sum(ea[i].elapsed_time(eb[i]) for i in range(args.steps)) / args.steps * 1e3
@@ -303,26 +347,36 @@ def bench_json_mask(args):
     if not args.no_check:
         from oracle import pyoracle
 
-        import numpy as np
-
         got = mask.cpu().numpy().view(np.uint32)
+        last = step_prefixes[total - 1]
         same = 0
         for r in range(0, rows, rows // 8):
             o = pyoracle.JsonOracle()
-            o.advance(prefixes[r])
+            o.advance(last[r])
             same += int((got[r] == o.mask(hv, V)).all())
         check = {"rows": 8, "mask_equal": same}
+    set_info = None
+    if mset is not None:
+        c = np.array(counts, dtype=np.float64)
+        set_info = {"capacity": 0 if mode == "dedupe" else 1024, "distinct_per_step": round(c[:, 1].mean(), 2),
+                    "hits_per_step": round(c[:, 2].mean(), 2), "evaluated_per_step": round(c[:, 3].mean(), 2),
+                    "host_us_per_fill": round(host_s / args.steps * 1e6, 1)}
+        mset.close()
     alg = int(hv.offsets.nbytes + hv.bytes.nbytes + hv.special.nbytes + rows * stride * 4)
     rec = {"metric": "JsonObject allow-masks per second (rows x 151936 tokens)", "value": round(rows / (us * 1e-6), 1),
            "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "dtype": "u8", "data": "synthetic",
-           "config": {"workload": "tsm_json_mask: 256 rows, states from random JSON prefixes, synthetic vocab",
-                      "rows": rows, "vocab": V},
+           "config": {"workload": ("tsm_json_mask: 256 rows, states from random JSON prefixes, synthetic vocab"
+                                   if mode != "decode" else
+                                   "tsm_json_masks_fill: 256 rows each writing a random JSON document, "
+                                   "one 4-byte token per step, synthetic vocab"),
+                      "rows": rows, "vocab": V, "mask_mode": mode, "mask_set": set_info},
            "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
                         "algorithmic_bytes_per_step": alg, "kernel_avg_us": round(us, 2),
-                        "kernel": "json_mask_kernel (one launch per step)"},
+                        "kernel": ("json_mask_kernel (one launch per step)" if mode == "direct" else
+                                   "json_mask_kernel over the step's new states + mask_copy_kernel")},
            "cpu_baseline": None, "oracle_check": check}
     print(json.dumps(rec), flush=True)
 

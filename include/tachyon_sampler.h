@@ -284,6 +284,52 @@ int tsm_json_is_complete(const tsm_json_state* s);
 int tsm_json_mask(void* stream, const tsm_vocab* vocab, const tsm_json_state* states, uint32_t rows,
                   uint32_t usable, uint32_t* mask, uint32_t mask_stride, char* err, size_t errlen);
 
+/*
+ * A mask set: tsm_json_mask for a serving loop, where many rows share a state
+ * (every row writing string text at one depth, say) and states recur from step
+ * to step.  Each call evaluates every distinct state of its rows once, keeps
+ * the masks of up to `capacity` states in device memory (least recently used
+ * out first), and fills each row's mask by a copy from its state's mask.  The
+ * masks written are the ones tsm_json_mask writes for the same states.
+ * Replaces: the same closure as tsm_json_mask (src/scheduler.rs:653-656),
+ * with the per-state reuse the reference's probing has no need of.
+ *
+ * tsm_json_masks_create allocates the set on `device` (GPU memory:
+ * capacity * ceil(ceil(usable / 32) / 64) * 256 bytes, plus about 2 * 44
+ * bytes per row of staging in pinned host memory, which the kernels read over
+ * the bus); `capacity` 0 keeps no
+ * masks between calls (rows sharing a state within a call still share one
+ * evaluation).  NULL on failure, with the reason in err.
+ *
+ * tsm_json_masks_fill: `states` is a HOST array of `rows` (<= max_rows)
+ * states, as tsm_json_advance keeps them; `mask` (device) gets one row per
+ * state, words [0, ceil(usable / 32)) of each written.  `stats` (may be NULL)
+ * receives the call's counts.  Queued on `stream`: at most one evaluation
+ * launch and one copy launch.  The call waits on the host only for the
+ * launches of the call before the last one (the staging alternates between
+ * two halves).  The slots are tied to the
+ * vocabulary's device pointers and n_tokens: a call with other ones empties
+ * the set first; after changing a vocabulary's bytes in place, call
+ * tsm_json_masks_reset.  Calls on one set must come from one host thread at a
+ * time and be queued on one stream (or ordered by the caller): a later call
+ * may overwrite a slot an earlier call's copies still read.
+ */
+typedef struct tsm_json_masks tsm_json_masks;
+typedef struct tsm_json_fill_stats {
+    uint32_t rows;       /* rows filled */
+    uint32_t distinct;   /* distinct states among them */
+    uint32_t hits;       /* distinct states whose mask the set already held */
+    uint32_t evaluated;  /* states evaluated by this call (distinct - hits) */
+} tsm_json_fill_stats;
+
+tsm_json_masks* tsm_json_masks_create(int device, uint32_t max_rows, uint32_t capacity, uint32_t usable, char* err,
+                                      size_t errlen);
+void tsm_json_masks_destroy(tsm_json_masks* set);
+void tsm_json_masks_reset(tsm_json_masks* set);
+int tsm_json_masks_fill(tsm_json_masks* set, void* stream, const tsm_vocab* vocab, const tsm_json_state* states,
+                        uint32_t rows, uint32_t* mask, uint32_t mask_stride, tsm_json_fill_stats* stats, char* err,
+                        size_t errlen);
+
 /* ---- the logits producer ------------------------------------------------
  * Tachyon's output layer for the rows that get logits: xb = rmsnorm(x[r])
  * in f32 (src/model.rs:702-709 over src/kernels.rs:522-528), then

@@ -58,6 +58,10 @@ class TsmJsonState(ctypes.Structure):
     ]
 
 
+class TsmJsonFillStats(ctypes.Structure):
+    _fields_ = [("rows", u32), ("distinct", u32), ("hits", u32), ("evaluated", u32)]
+
+
 class TsmVocab(ctypes.Structure):
     _fields_ = [
         ("bytes", vp),
@@ -70,7 +74,8 @@ class TsmVocab(ctypes.Structure):
 
 SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version",
            "tsm_row_kind", "tsm_sample_static", "tsm_json_init", "tsm_json_advance", "tsm_json_accepts",
-           "tsm_json_is_complete", "tsm_json_mask", "tsm_lm_head_workspace", "tsm_lm_head"]
+           "tsm_json_is_complete", "tsm_json_mask", "tsm_json_masks_create", "tsm_json_masks_destroy",
+           "tsm_json_masks_reset", "tsm_json_masks_fill", "tsm_lm_head_workspace", "tsm_lm_head"]
 LM_SPLIT = 1
 ROWKIND_SPLIT = 1
 ROWKIND_WHOLE = 2
@@ -122,6 +127,15 @@ def lib():
         L.tsm_json_mask.restype = ctypes.c_int
         L.tsm_json_mask.argtypes = [vp, ctypes.POINTER(TsmVocab), vp, u32, u32, vp, u32, ctypes.c_char_p,
                                     ctypes.c_size_t]
+        L.tsm_json_masks_create.restype = vp
+        L.tsm_json_masks_create.argtypes = [ctypes.c_int, u32, u32, u32, ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_json_masks_destroy.restype = None
+        L.tsm_json_masks_destroy.argtypes = [vp]
+        L.tsm_json_masks_reset.restype = None
+        L.tsm_json_masks_reset.argtypes = [vp]
+        L.tsm_json_masks_fill.restype = ctypes.c_int
+        L.tsm_json_masks_fill.argtypes = [vp, vp, ctypes.POINTER(TsmVocab), ctypes.POINTER(TsmJsonState), u32, vp,
+                                          u32, ctypes.POINTER(TsmJsonFillStats), ctypes.c_char_p, ctypes.c_size_t]
         L.tsm_lm_head_workspace.restype = ctypes.c_size_t
         L.tsm_lm_head_workspace.argtypes = [u32, u32, u32]
         L.tsm_lm_head.restype = ctypes.c_int

@@ -103,6 +103,60 @@ def json_mask(vocab: DeviceVocab, states_dev, rows: int, usable: int, mask_dev, 
         raise _lib.TsmError(err.value.decode())
 
 
+class JsonMaskSet:
+    """tsm_json_masks_*: masks of recent JsonObject states kept on the GPU;
+    each fill evaluates every distinct state of its rows once (reusing the
+    kept ones) and copies each row's mask from its state's."""
+
+    def __init__(self, max_rows: int, capacity: int, usable: int, device: int = 0):
+        err = _lib._err()
+        self.handle = _lib.lib().tsm_json_masks_create(device, max_rows, capacity, usable, err, len(err))
+        if not self.handle:
+            raise _lib.TsmError(err.value.decode())
+        self.usable = usable
+
+    def fill(self, vocab: DeviceVocab, states, mask_dev, mask_stride: int, stream=None):
+        """Masks of the rows whose host states are `states` (a sequence of
+        JsonConstraint or of packed 12-byte states, or an array from pack())
+        into mask_dev; returns the call's counts (rows, distinct, hits,
+        evaluated)."""
+        import torch
+
+        arr = states if isinstance(states, ctypes.Array) else self.pack(states)
+        s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        vb = vocab.abi()
+        st = _lib.TsmJsonFillStats()
+        err = _lib._err()
+        rc = _lib.lib().tsm_json_masks_fill(self.handle, ctypes.c_void_p(s), ctypes.byref(vb), arr, len(arr),
+                                            ctypes.c_void_p(mask_dev.data_ptr()), mask_stride, ctypes.byref(st),
+                                            err, len(err))
+        if rc != 0:
+            raise _lib.TsmError(err.value.decode())
+        return (st.rows, st.distinct, st.hits, st.evaluated)
+
+    @staticmethod
+    def pack(states):
+        """The host array fill() takes: JsonConstraint or packed 12-byte states."""
+        packed = [c.packed() if isinstance(c, JsonConstraint) else bytes(c) for c in states]
+        arr = (_lib.TsmJsonState * len(packed))()
+        ctypes.memmove(arr, b"".join(packed), 12 * len(packed))
+        return arr
+
+    def reset(self):
+        _lib.lib().tsm_json_masks_reset(self.handle)
+
+    def close(self):
+        if self.handle:
+            _lib.lib().tsm_json_masks_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def pack_states(constraints) -> np.ndarray:
     """The rows' packed states, ready to upload (uint8, 12 bytes per row)."""
     return np.frombuffer(b"".join(c.packed() for c in constraints), np.uint8).copy()

@@ -143,3 +143,122 @@ def test_json_mask_rejects_bad_arguments(vocab):
         json_mask(dv, st, 1, 1000, mask, 8)
     with pytest.raises(_lib.TsmError, match="rows"):
         json_mask(dv, st, 0, 100, mask, 8)
+
+
+def state_key(c):
+    """A state's identity: its packed bytes without the padding."""
+    return c.packed()[:9]
+
+
+def test_json_mask_set_matches_the_direct_producer(vocab):
+    """tsm_json_masks_fill writes every row's mask equal to tsm_json_mask's for
+    the same state, over calls that hit, miss and overflow the kept masks:
+    first call 80 rows of ~40 states into a set keeping 8 (the first 8
+    distinct states get slots, the rest are evaluated straight into their
+    rows), then a call of 3 kept states and 5 new ones, then the same rows
+    again, a set keeping nothing, and a new vocabulary (nothing reused)."""
+    import torch
+
+    from tachyon_amd.constrain import DeviceVocab, JsonConstraint, JsonMaskSet
+
+    hv, dv = vocab
+    V = hv.n_tokens
+    nw = (V + 31) // 32
+    stride = nw + 2
+    prefixes = wl.json_prefixes(48, seed=0x15A6)
+    cs, _ = states_for(prefixes)
+    rng = np.random.default_rng(0x15A7)
+    rows1 = [cs[i] for i in rng.integers(0, len(cs), 80)]
+    # a state with stray padding bytes is the same state
+    odd = JsonConstraint()
+    odd.advance(prefixes[5])
+    odd.state.pad[0] = 0xAB
+    rows1[-1] = odd
+
+    def distinct(rows):
+        keys = []
+        for c in rows:
+            if state_key(c) not in keys:
+                keys.append(state_key(c))
+        return keys
+
+    def fill(ms, rows, vocab_dev=dv):
+        mask = torch.full((len(rows), stride), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+        st = ms.fill(vocab_dev, rows, mask, stride)
+        torch.cuda.synchronize()
+        return mask.cpu().numpy().view(np.uint32), st
+
+    def check_rows(got, rows):
+        ref = produce(dv, rows, V, stride)
+        for r in range(len(rows)):
+            bad = np.nonzero(got[r, :nw] != ref[r, :nw])[0]
+            assert bad.size == 0, (r, bad[:5])
+            assert (got[r, nw:] == 0x5A5A5A5A).all(), r
+
+    ms = JsonMaskSet(max_rows=128, capacity=8, usable=V)
+    try:
+        k1 = distinct(rows1)
+        say(f"[gpu] mask set: call 1, {len(rows1)} rows, {len(k1)} states, 8 kept")
+        got, st = fill(ms, rows1)
+        check_rows(got, rows1)
+        assert st == (80, len(k1), 0, len(k1)), st
+        # the first 8 distinct states of call 1 hold the slots
+        first = {k: next(c for c in rows1 if state_key(c) == k) for k in k1}
+        kept = [first[k] for k in k1[:3]]
+        others, _ = states_for(wl.json_prefixes(96, seed=0x15A8))
+        fresh, seen = [], set(k1)
+        for c in others:
+            if state_key(c) not in seen:
+                seen.add(state_key(c))
+                fresh.append(c)
+        fresh = fresh[:5]
+        assert len(fresh) == 5
+        # the kept states first: each new state then takes the slot of one of
+        # call 1's states 4-8, the least recently used
+        rows2 = [kept[0], kept[1], kept[2], fresh[0], kept[0], fresh[1], fresh[2], fresh[3], fresh[4], fresh[0]]
+        say("[gpu] mask set: call 2, 10 rows, 3 kept states and 5 new")
+        got, st = fill(ms, rows2)
+        check_rows(got, rows2)
+        assert st == (10, 8, 3, 5), st
+        say("[gpu] mask set: call 3, call 2's rows again")
+        got, st = fill(ms, rows2)
+        check_rows(got, rows2)
+        assert st == (10, 8, 8, 0), st
+        # another vocabulary (other device pointers): nothing is reused
+        dv2 = DeviceVocab(hv)
+        got, st = fill(ms, rows2, dv2)
+        check_rows(got, rows2)
+        assert st == (10, 8, 0, 8), st
+    finally:
+        ms.close()
+    ms0 = JsonMaskSet(max_rows=128, capacity=0, usable=V)
+    try:
+        say("[gpu] mask set: capacity 0, call 1's rows")
+        got, st = fill(ms0, rows1)
+        check_rows(got, rows1)
+        assert st == (80, len(k1), 0, len(k1)), st
+        got, st = fill(ms0, rows1[:7])
+        check_rows(got, rows1[:7])
+        assert st[2] == 0, st
+    finally:
+        ms0.close()
+
+
+def test_json_mask_set_rejects_bad_arguments(vocab):
+    import torch
+
+    from tachyon_amd import _lib
+    from tachyon_amd.constrain import JsonConstraint, JsonMaskSet
+
+    hv, dv = vocab
+    with pytest.raises(_lib.TsmError, match="max_rows"):
+        JsonMaskSet(max_rows=0, capacity=4, usable=100)
+    ms = JsonMaskSet(max_rows=4, capacity=4, usable=1000)
+    try:
+        mask = torch.zeros(8, 40, dtype=torch.int32, device="cuda")
+        with pytest.raises(_lib.TsmError, match="rows"):
+            ms.fill(dv, [JsonConstraint()] * 5, mask, 40)
+        with pytest.raises(_lib.TsmError, match="mask_stride"):
+            ms.fill(dv, [JsonConstraint()], mask, 31)
+    finally:
+        ms.close()
