@@ -1670,6 +1670,7 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
         // whenever it is <= W), and the window boundary is not needed.
         uint64_t ta = ~0ull;
         bool fast = false, sorted = false;
+        uint32_t nal_sorted = 0;  // keys in lds_rsorted() when sorted
         if (m.constrained) {
             // the window list's allowed keys, ranked against each other when
             // at most kRankMax: the want-th is then read off, and the kept list
@@ -1686,13 +1687,15 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
                 if (in && at < kRankMax) rk[at] = c;
                 nal += static_cast<uint32_t>(__popcll(b));
             }
-            if (nal <= kRankMax && nal >= m.want) {
+            if (nal <= kRankMax && nal > 0u) {
                 if (lane < 8u) rk[nal + lane] = ~0ull;  // the pad to a multiple of 8
                 __builtin_amdgcn_wave_barrier();
                 wave_rank_sort(nal);
-                ta = lds_rsorted()[m.want - 1u];
+                // fewer than `want` allowed keys listed: no want-th (not fast)
+                ta = nal >= m.want ? lds_rsorted()[m.want - 1u] : ~0ull;
                 sorted = true;
-            } else {
+                nal_sorted = nal;
+            } else if (nal > kRankMax) {
                 __builtin_amdgcn_wave_barrier();
                 ta = wave_kth_reg(nwin, m.want, allowed_c);
             }
@@ -1708,8 +1711,33 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             }
         }
         uint32_t g;
+        bool prefix = false;  // the kept list is lds_rsorted()[0..g)
         if (fast && sorted) {
             g = m.want;  // lds_rsorted()[0..want): the kept list, in order
+            prefix = true;
+        } else if (m.constrained && sorted) {
+            // fewer than `want` allowed ids rank inside the window: the kept
+            // list is every allowed id inside it (sampler.rs:209-210), which
+            // is the prefix of the sorted allowed keys at or below the window
+            // boundary
+            const uint64_t tw = wave_kth_reg(nwin, m.window, canon_all);
+            uint32_t inw = 0;
+            for (uint32_t i = lane; i < nal_sorted; i += kWave) inw += lds_rsorted()[i] <= tw ? 1u : 0u;
+            inw = wave_sum_dpp(inw);
+            if (inw > 0) {
+                g = min(inw, m.want);
+                prefix = true;
+            } else {
+                // none in the window: the best allowed ids of the whole row by
+                // f32::total_cmp (sampler.rs:211-221)
+                auto allowed_total = [&](uint32_t r, uint64_t* c) {
+                    if (!(wl[r].y & kEntAllowed)) return false;
+                    *c = composite(total_key(__uint_as_float(wl[r].x)), wl[r].y & kEntId);
+                    return true;
+                };
+                const uint64_t tf = wave_kth_reg(nwin, m.want, allowed_total);
+                g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return allowed_total(r, c) && *c <= tf; });
+            }
         } else if (fast) {
             g = wave_gather_reg(nwin, [&](uint32_t r, uint64_t* c) { return allowed_c(r, c) && *c <= ta; });
         } else if (!m.constrained) {
@@ -1747,8 +1775,8 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             }
         }
         const uint32_t len = min(g, m.want);
-        const uint64_t mine = (fast && sorted) ? (lane < len ? lds_rsorted()[lane] : ~0ull)
-                                               : wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
+        const uint64_t mine = prefix ? (lane < len ? lds_rsorted()[lane] : ~0ull)
+                                     : wave_sort_rank(lane < g ? lds_wlist()[lane] : ~0ull, g);
         if (len == 0) {
             pk.token = 0xFFFFFFFFu;  // nothing to rank (e.g. NaN logits): flagged below
         } else {
