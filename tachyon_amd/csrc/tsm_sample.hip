@@ -1724,8 +1724,20 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             uint32_t inw = 0;
             for (uint32_t i = lane; i < nal_sorted; i += kWave) inw += lds_rsorted()[i] <= tw ? 1u : 0u;
             inw = wave_sum_dpp(inw);
+            // with no value +-0 among them, the best allowed ids by
+            // f32::total_cmp (the fallback below) are the sorted prefix too:
+            // the two orders differ only between -0 and +0
+            const uint32_t lf = min(nal_sorted, m.want);
+            auto is_zero = [&](uint32_t i) {
+                return static_cast<uint32_t>(lds_rsorted()[i] >> 32) == ~canon_key(0.0f);
+            };
+            // the kept ones and the first one after them
+            const bool zero = (lane < lf && is_zero(lane)) || (lane == 0 && lf < nal_sorted && is_zero(lf));
             if (inw > 0) {
                 g = min(inw, m.want);
+                prefix = true;
+            } else if (!wave_ballot(zero)) {
+                g = lf;  // none in the window: the row's best allowed ids (sampler.rs:211-221)
                 prefix = true;
             } else {
                 // none in the window: the best allowed ids of the whole row by

@@ -331,6 +331,30 @@ def window_case(seed, vocab, rows=1, top_k=1024, hist_len=10, repetition_penalty
     return Workload(f"window{seed}", x, vocab, p, ids, offs, mask, uniforms(rng, rows), top_stride=8)
 
 
+def below_window_case(seed, vocab=6000, rows=20):
+    """Constrained top-k rows (k = 40, window 256; 20 rows, beyond the
+    split kernel's batches) whose allowed ids all lie below the window: the other ids sit around 6, the allowed ones (60 to
+    120 a row) take +0, -0, -1 or -2 (even rows) or N(-3, 1) values (odd
+    rows), so the kept list comes from the fallback over the whole row
+    (sampler.rs:211-221), where f32::total_cmp puts +0 before -0."""
+    rng = np.random.default_rng(seed)
+    x = (6.0 + rng.standard_normal((rows, vocab))).astype(np.float32)
+    allowed = np.zeros((rows, vocab), bool)
+    for r in range(rows):
+        ids = rng.choice(vocab, int(rng.integers(60, 121)), replace=False)
+        allowed[r, ids] = True
+        if r % 2 == 0:
+            x[r, ids] = rng.choice(np.array([0.0, -0.0, -1.0, -2.0], np.float32), len(ids))
+        else:
+            x[r, ids] = (rng.standard_normal(len(ids)) - 3.0).astype(np.float32)
+    p = make_params(rows, temperature=0.8, top_k=40, top_p=0.9, flags=ROW_CONSTRAINED | ROW_LOGPROBS,
+                    n_logprobs=5)
+    p["min_p"][1::4] = 0.05
+    ids, offs = uniform_histories(rng, rows, 32, vocab)
+    p["repetition_penalty"][::3] = 1.2
+    return Workload(f"below{seed}", x, vocab, p, ids, offs, pack_mask(allowed), uniforms(rng, rows), top_stride=5)
+
+
 def cluster_case(seed, vocab=151936, rows=4, width=0.025, temperature=3.0, top_p=0.9, sigma=3.0):
     """Nucleus rows (no top-k) whose first third of the vocabulary sits in a
     dense Gaussian cluster about `width` wide at 3.0, beside N(0, sigma^2)

@@ -60,6 +60,14 @@ def test_emu_parity_wide_windows(case):
     run_case(wl.window_case(**case), f"emu window{case['seed']}")
 
 
+@pytest.mark.parametrize("seed,rows", [(50, 20), (51, 20), (52, 8)])
+def test_emu_parity_allowed_below_the_window(seed, rows):
+    """Allowed ids only below the window, some valued +0 and -0: the
+    fallback's f32::total_cmp order (+0 before -0) against the window's
+    (20 rows: the whole-row kernel; 8: the split kernel)."""
+    run_case(wl.below_window_case(seed, rows=rows), f"emu below{seed}")
+
+
 @pytest.mark.parametrize("name,rows", [("c1", 1), ("c2", 8), ("c3", 4), ("c4", 4), ("c5", 4)])
 def test_emu_parity_configs(name, rows):
     """BASELINE shapes at full vocabulary with few rows.  c2's rows come in

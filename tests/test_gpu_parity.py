@@ -119,6 +119,14 @@ def test_parity_dense_clusters(ctx):
         run_case(ctx, w, label)
 
 
+def test_parity_allowed_below_the_window(ctx):
+    """Constrained top-k rows whose allowed ids all rank below the window
+    (sampler.rs:211-221: the best allowed ids of the whole row by
+    f32::total_cmp), some with +0 and -0 among the kept values."""
+    for seed, rows in ((50, 20), (51, 20), (52, 8)):
+        run_case(ctx, wl.below_window_case(seed, rows=rows), f"below{seed}")
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
 def test_parity_baseline_configs(ctx, name):
     w = wl.CONFIGS[name]()
@@ -137,22 +145,6 @@ def _rows_of(w, sel, name):
     return wl.Workload(name, np.ascontiguousarray(w.logits[sel]), w.usable, w.params[sel].copy(), hist_ids, hist_off,
                        None if w.mask is None else np.ascontiguousarray(w.mask[sel]), w.uniforms[sel].copy(),
                        top_stride=w.top_stride)
-
-
-@pytest.mark.parametrize("case", WINDOW_CASES, ids=[f"window{c['seed']}" for c in WINDOW_CASES])
-def test_parity_wide_windows(ctx, case):
-    """Top-k windows near 1024 over small vocabularies: split-row segments
-    whose candidates exceed the segment's area take the exact thresholds."""
-    run_case(ctx, wl.window_case(**case), f"window{case['seed']}")
-
-
-def test_parity_dense_clusters(ctx):
-    """Nucleus rows whose dense cluster once overflowed a census round
-    (sweep batches 193 and 272) and eight synthetic rows of that kind."""
-    from parity import dense_cluster_workloads
-
-    for label, w in dense_cluster_workloads():
-        run_case(ctx, w, label)
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
