@@ -1373,6 +1373,7 @@ __device__ __forceinline__ uint64_t wave_sort_rank(uint64_t v, uint32_t n) {
 // step with loads every lane makes at the same address, and writes it at its
 // rank in lds_rsorted().  n / 8 steps of 8K compares per lane.
 constexpr uint32_t kRankMax = 256;
+constexpr uint32_t kRankCut = 96;  // more allowed keys than this: only those at or below a cut are sorted
 __device__ __forceinline__ uint64_t* lds_rkeys() { return reinterpret_cast<uint64_t*>(lds_base() + kOffHist + 4096); }
 __device__ __forceinline__ uint64_t* lds_rsorted() { return lds_rkeys() + kRankMax + 8; }
 static_assert(4096 + (2 * kRankMax + 8) * 8 <= kBins * 12, "rank sort scratch fits the histogram region");
@@ -1671,17 +1672,47 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
         uint64_t ta = ~0ull;
         bool fast = false, sorted = false;
         uint32_t nal_sorted = 0;  // keys in lds_rsorted() when sorted
+        uint64_t cut = ~0ull;     // the allowed keys above it are not in lds_rsorted()
         if (m.constrained) {
             // the window list's allowed keys, ranked against each other when
             // at most kRankMax: the want-th is then read off, and the kept list
             // is the sorted prefix
             uint32_t nal = 0;
             uint64_t* rk = lds_rkeys();
+            // Of many allowed keys only the best want + 1 matter (the kept
+            // list, ta, and the first key after the kept ones).  Each lane's
+            // best is a distinct key, so at least ci + 1 keys lie at or below
+            // the (ci+1)-th best of the lanes' bests (ci = want, or 63 when
+            // want is 64), and the keys above that cut are left out of the
+            // sort.  (A row that is not fast has fewer than want allowed keys
+            // inside the window, so its window boundary lies below the cut
+            // too.)
+            const uint32_t ci = min(m.want, static_cast<uint32_t>(kWave) - 1u);
+            {
+                uint64_t lb = ~0ull;
+                uint32_t cnt = 0;
+#pragma unroll
+                for (uint32_t r = 0; r < kWaveRegs; r++) {
+                    if (r * kWave >= nwin) break;
+                    uint64_t c = 0;
+                    if (r * kWave + lane < nwin && allowed_c(r, &c)) {
+                        lb = c < lb ? c : lb;
+                        cnt++;
+                    }
+                }
+                const uint32_t lanes = static_cast<uint32_t>(__popcll(wave_ballot(lb != ~0ull)));
+                if (wave_sum_dpp(cnt) > kRankCut && lanes > ci) {
+                    // lanes without an allowed key hold ~0 and sort last
+                    const uint64_t srt = wave_sort_rank(lb, kWave);
+                    cut = (static_cast<uint64_t>(wave_read(static_cast<uint32_t>(srt >> 32), ci)) << 32) |
+                          wave_read(static_cast<uint32_t>(srt), ci);
+                }
+            }
 #pragma unroll
             for (uint32_t r = 0; r < kWaveRegs; r++) {
                 if (r * kWave >= nwin) break;
                 uint64_t c = 0;
-                const bool in = r * kWave + lane < nwin && allowed_c(r, &c);
+                const bool in = r * kWave + lane < nwin && allowed_c(r, &c) && c <= cut;
                 const uint64_t b = wave_ballot(in);
                 const uint32_t at = nal + lanes_below(b);
                 if (in && at < kRankMax) rk[at] = c;
@@ -1731,8 +1762,10 @@ __device__ __forceinline__ bool finish_wave(const SampleArgs& a, const Fin& f, c
             auto is_zero = [&](uint32_t i) {
                 return static_cast<uint32_t>(lds_rsorted()[i] >> 32) == ~canon_key(0.0f);
             };
-            // the kept ones and the first one after them
-            const bool zero = (lane < lf && is_zero(lane)) || (lane == 0 && lf < nal_sorted && is_zero(lf));
+            // the kept ones and the first one after them (when the cut left
+            // that one out, the check cannot be made: the general path)
+            const bool zero = (lane < lf && is_zero(lane)) || (lane == 0 && lf < nal_sorted && is_zero(lf)) ||
+                              (lane == 0 && lf == nal_sorted && cut != ~0ull);
             if (inw > 0) {
                 g = min(inw, m.want);
                 prefix = true;
