@@ -1,8 +1,10 @@
 #!/usr/bin/env python3
 """Benchmark of the batched sampling path on one MI355X.
 
-A step is one tsm_sample() call (one sample_kernel launch) over one batch of
-synthetic logits already resident in HBM.  The default workload is BASELINE
+A step is one tsm_sample() call over one batch of synthetic logits already
+resident in HBM: one launch of the kernel that takes the batch's rows
+(topk_kernel for c3 and c4, whose rows are all of the lean kind;
+sample_kernel for c5; both for c2's mixed rows; split_kernel for c1).  The default workload is BASELINE
 config c4, the headline: B=256, V=151936, repetition 1.1 + presence 0.4 +
 frequency 0.2 over 1024-token Zipf histories, a 30% grammar mask, T=0.7,
 top_k=64, top_p=0.92, min_p=0.02 and top-5 logprobs.
@@ -53,9 +55,9 @@ DESCR = {
 # for their top-k rows)
 KERNELS = {
     "c1": "split_kernel (one launch per tsm_sample step)",
-    "c2": "sample_kernel (one launch per tsm_sample step)",
-    "c3": "sample_kernel (one launch per tsm_sample step)",
-    "c4": "sample_kernel (one launch per tsm_sample step)",
+    "c2": "topk_kernel + sample_kernel (two launches per tsm_sample step: lean and general rows)",
+    "c3": "topk_kernel (one launch per tsm_sample step: every row of the lean kind)",
+    "c4": "topk_kernel (one launch per tsm_sample step: every row of the lean kind)",
     "c5": "sample_kernel (one launch per tsm_sample step)",
 }
 

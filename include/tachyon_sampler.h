@@ -194,7 +194,7 @@ int tsm_distribution(tsm_ctx* ctx, void* stream, const tsm_batch* batch,
                                           values near one fold event than the
                                           exact folds' census takes (2048).
                                           Fallback: sample that row with the
-                                          CPU Sampler, as INTEGRATION.md says */
+                                          reference's CPU Sampler */
 #define TSM_STATUS_ROW_KIND        16u /* a row of a kind the batch's row_kinds
                                           left out: token 0 written           */
 int tsm_status(tsm_ctx* ctx, uint32_t* status, char* err, size_t errlen);

@@ -1,4 +1,4 @@
-"""HBM traffic of the sampling kernel from rocprofv3 counter passes.
+"""HBM traffic of a sampling kernel from rocprofv3 counter passes.
 
 rocprofv3 collects FETCH_SIZE and WRITE_SIZE (KiB per dispatch) in separate
 runs: one pair over ``bench.py`` (the sampling kernel) and one pair over
@@ -11,7 +11,7 @@ Usage (paths are the ``*_counter_collection.csv`` files rocprofv3 wrote):
 
     python -m tachyon_amd.traffic --kernel-fetch K_F.csv --kernel-write K_W.csv \\
         --copy-fetch C_F.csv --copy-write C_W.csv --copy-mb 512 \\
-        --algorithmic-bytes 161506304 --out traffic_c4.json
+        --algorithmic-bytes 161506304 --kernel topk_kernel --out traffic_c4.json
 
 It prints a short text summary and writes the JSON that ``bench.py`` reads
 for ``roofline.traffic``.  The JSON carries the SHA-256 of the sampling
@@ -28,7 +28,7 @@ import json
 import os
 import statistics
 
-KERNEL = "sample_kernel"
+KERNEL = "topk_kernel"  # c4's rows all take the lean whole-row kernel
 DEFAULT_LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libtachyon_sampler.so")
 
 
@@ -81,6 +81,7 @@ def main() -> None:
     ap.add_argument("--algorithmic-bytes", type=int, required=True)
     ap.add_argument("--out", required=True)
     ap.add_argument("--library", default=DEFAULT_LIBRARY, help="the library the counter runs loaded")
+    ap.add_argument("--kernel", default=KERNEL, help="a part of the kernel's name (its dispatches are counted)")
     args = ap.parse_args()
 
     copy_bytes = args.copy_mb << 20
@@ -89,15 +90,16 @@ def main() -> None:
     cw = statistics.median(copy_kernel_values(args.copy_write, "WRITE_SIZE"))
     f_fetch = copy_bytes / (cf * 1024.0)
     f_write = copy_bytes / (cw * 1024.0)
-    kf = per_dispatch(args.kernel_fetch, "FETCH_SIZE", KERNEL)
-    kw = per_dispatch(args.kernel_write, "WRITE_SIZE", KERNEL)
+    kf = per_dispatch(args.kernel_fetch, "FETCH_SIZE", args.kernel)
+    kw = per_dispatch(args.kernel_write, "WRITE_SIZE", args.kernel)
     if not kf or not kw:
-        raise SystemExit("no sample_kernel dispatches in the counter files")
+        raise SystemExit(f"no {args.kernel} dispatches in the counter files")
     fetch_b = statistics.mean(kf) * 1024.0 * f_fetch
     write_b = statistics.mean(kw) * 1024.0 * f_write
     total = fetch_b + write_b
     rec = {
         "library_sha256": library_sha256(args.library),
+        "kernel": args.kernel,
         "hbm_bytes_per_step": int(round(total)),
         "fetch_bytes_per_step": int(round(fetch_b)),
         "write_bytes_per_step": int(round(write_b)),
@@ -112,7 +114,7 @@ def main() -> None:
     with open(args.out, "w") as fh:
         json.dump(rec, fh, indent=1)
         fh.write("\n")
-    print(f"sample_kernel: fetch {fetch_b / 1e6:.2f} MB + write {write_b / 1e6:.3f} MB per launch "
+    print(f"{args.kernel}: fetch {fetch_b / 1e6:.2f} MB + write {write_b / 1e6:.3f} MB per launch "
           f"= {total / 1e6:.2f} MB; algorithmic {args.algorithmic_bytes / 1e6:.2f} MB "
           f"(ratio {total / args.algorithmic_bytes:.3f}); copy calibration factors fetch {f_fetch:.3f} "
           f"write {f_write:.3f}")

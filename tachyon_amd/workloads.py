@@ -62,7 +62,7 @@ class Workload:
         return 0 if self.mask is None else int(self.mask.shape[1])
 
     def algorithmic_bytes(self) -> int:
-        """Bytes one step must move at least (BASELINE.md's count): one read
+        """Bytes one step must move at least (the headline metric's count): one read
         of every usable logit, the mask words of constrained rows, the history
         ids, the uniforms, and the outputs (token, plus logprob and n top
         (id, logprob) pairs for rows that ask for logprobs)."""
@@ -333,10 +333,11 @@ def window_case(seed, vocab, rows=1, top_k=1024, hist_len=10, repetition_penalty
 
 def below_window_case(seed, vocab=6000, rows=20):
     """Constrained top-k rows (k = 40, window 256; 20 rows, beyond the
-    split kernel's batches) whose allowed ids all lie below the window: the other ids sit around 6, the allowed ones (60 to
-    120 a row) take +0, -0, -1 or -2 (even rows) or N(-3, 1) values (odd
-    rows), so the kept list comes from the fallback over the whole row
-    (sampler.rs:211-221), where f32::total_cmp puts +0 before -0."""
+    split kernel's batches) whose allowed ids all lie below the window: the
+    other ids sit around 6, the allowed ones (60 to 120 a row) take +0, -0,
+    -1 or -2 (even rows) or N(-3, 1) values (odd rows), so the kept list
+    comes from the fallback over the whole row (sampler.rs:211-221), where
+    f32::total_cmp puts +0 before -0."""
     rng = np.random.default_rng(seed)
     x = (6.0 + rng.standard_normal((rows, vocab))).astype(np.float32)
     allowed = np.zeros((rows, vocab), bool)
