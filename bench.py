@@ -98,7 +98,7 @@ def cpu_baseline(w, budget_s, threads):
         pyoracle.sample_batch(w, nthreads=threads)
         steps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 50:
+        if el >= budget_s or steps >= 1000:
             break
     return w.rows * steps / el, steps, el
 

@@ -107,7 +107,9 @@ typedef struct tsm_batch {
  * batch did not name is not sampled and sets TSM_STATUS_ROW_KIND.
  * tsm_row_kind() gives a row's kind from the same fields the device reads:
  * its parameters, the batch's `usable`, the row's history length and whether
- * the batch has a mask.
+ * the batch has a mask.  In a batch of up to 16 rows, a row whose kind holds
+ * TSM_ROWKIND_SPLIT need add only that bit to the batch's row_kinds (its
+ * other bit names the whole-row kernel that takes it in a larger batch).
  */
 #define TSM_ROWKIND_SPLIT 1u /* the split-row kernel (batches of up to 16 rows)      */
 #define TSM_ROWKIND_WHOLE 2u /* the general whole-row kernel                         */

@@ -2542,9 +2542,13 @@ __device__ __forceinline__ void sample_row(const SampleArgs& a) {
     if constexpr (kLean) {
         // the single-wave finish; the rare rows it cannot take go through the
         // out-of-line general finishes (their arguments through LDS)
+        // (a lean row writes no distribution: its pointers are not passed,
+        // so they need not stay live through the row)
         if (row_has_nan()) {
             if (tid == 0) {
                 nan_call()->a = a;
+                nan_call()->a.dist_ids = nullptr;
+                nan_call()->a.dist_probs = nullptr;
                 nan_call()->f = f;
                 nan_call()->nlp = nlp;
             }
@@ -2557,6 +2561,8 @@ __device__ __forceinline__ void sample_row(const SampleArgs& a) {
             return;
         if (tid == 0) {
             row_call()->a = a;
+            row_call()->a.dist_ids = nullptr;
+            row_call()->a.dist_probs = nullptr;
             row_call()->f = f;
             row_call()->tg0 = tg0;
             row_call()->nlp = nlp;

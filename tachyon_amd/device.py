@@ -45,17 +45,26 @@ class DeviceBatch:
         return 0 if self.mask is None else int(self.mask.shape[1])
 
 
+SPLIT_ROWS_MAX = 16  # batches of at most this many rows run the split-row kernel
+
+
 def row_kinds(w: Workload, has_mask: bool) -> int:
     """OR of tsm_row_kind() over the workload's rows, from its host-side
-    parameters and history lengths (what a caller knows before the step)."""
+    parameters and history lengths (what a caller knows before the step).
+    In a batch small enough for the split-row kernel, a row it takes adds
+    only TSM_ROWKIND_SPLIT (its other bit names the whole-row kernel that
+    would take it in a larger batch), so no whole-row kernel is queued for
+    nothing."""
     L = _lib.lib()
     params = np.ascontiguousarray(w.params)
     hl = np.zeros(w.rows, np.int64) if w.hist_offsets is None else np.diff(w.hist_offsets.astype(np.int64))
     kinds = 0
     base = params.ctypes.data
+    small = w.rows <= SPLIT_ROWS_MAX
     for r in range(w.rows):
-        kinds |= int(L.tsm_row_kind(ctypes.c_void_p(base + r * params.itemsize), w.usable, int(hl[r]),
-                                    1 if has_mask else 0))
+        k = int(L.tsm_row_kind(ctypes.c_void_p(base + r * params.itemsize), w.usable, int(hl[r]),
+                               1 if has_mask else 0))
+        kinds |= _lib.ROWKIND_SPLIT if (small and k & _lib.ROWKIND_SPLIT) else k
     return kinds
 
 
