@@ -25,7 +25,8 @@ def build(target="emu_driver"):
 
     with open(os.path.join(EMU_DIR, ".build.lock"), "w") as lock:
         fcntl.flock(lock, fcntl.LOCK_EX)
-        subprocess.run(["make", "-s", "-C", EMU_DIR, target], check=True)
+        jobs = str(max(1, min(5, len(os.sched_getaffinity(0)))))
+        subprocess.run(["make", "-s", "-j", jobs, "-C", EMU_DIR, target], check=True)
     return os.path.join(EMU_DIR, target)
 
 
