@@ -450,6 +450,10 @@ hipError_t hipHostMalloc(void** p, size_t n, unsigned) {
     *p = std::malloc(n);
     return *p ? hipSuccess : hipErrorOutOfMemory;
 }
+hipError_t hipHostGetDevicePointer(void** d, void* h, unsigned) {
+    *d = h;
+    return h ? hipSuccess : hipErrorInvalidValue;
+}
 hipError_t hipHostFree(void* p) {
     std::free(p);
     return hipSuccess;

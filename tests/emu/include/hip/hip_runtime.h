@@ -314,6 +314,9 @@ hipError_t hipEventDestroy(hipEvent_t e);
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t s = nullptr);
 hipError_t hipEventSynchronize(hipEvent_t e);
 hipError_t hipHostMalloc(void** p, size_t n, unsigned flags = 0);
+#define hipHostMallocMapped 0x2u
+// pinned host memory is the device's memory here: its device address is itself
+hipError_t hipHostGetDevicePointer(void** d, void* h, unsigned flags);
 hipError_t hipHostFree(void* p);
 hipError_t hipGetLastError();
 const char* hipGetErrorString(hipError_t e);

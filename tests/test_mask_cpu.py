@@ -52,3 +52,18 @@ def test_advance_through_rejected_bytes_matches():
         assert c.is_complete() == o.is_complete()
         for t in probes:
             assert c.accepts(t) == o.accepts(t), (junk, t)
+
+
+def test_mask_set_on_the_cpu_emulation():
+    """The mask producer's sources on the CPU emulation (AddressSanitizer):
+    tsm_json_masks_fill against tsm_json_mask and the host stepping of
+    tsm_json_accepts, over calls that hit, miss and overflow a set keeping 4
+    states, a changed vocabulary and a set keeping nothing, with the call
+    counts (distinct, kept, evaluated) each call must report."""
+    import subprocess
+
+    import emu_harness as E
+
+    exe = E.build("emu_mask")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stderr[-3000:]
