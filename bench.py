@@ -127,6 +127,8 @@ def main():
     ap.add_argument("--lm-rows", type=int, default=256, help="with --lm-head: logit rows per call (256: the c4 batch)")
     ap.add_argument("--lm-bf16", action="store_true",
                     help="with --lm-head: activations rounded to bf16 (default: the hi/lo split)")
+    ap.add_argument("--lm-q8", action="store_true",
+                    help="with --lm-head: a Q8 lm_head (tsm_lm_head_q8: int8 weights, an f16 scale per 32)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run N MiB device copies for counter calibration instead of the bench")
     args = ap.parse_args()
@@ -149,7 +151,10 @@ def main():
         return
 
     if args.lm_head:
-        bench_lm_head(args)
+        if args.lm_q8:
+            bench_lm_head_q8(args)
+        else:
+            bench_lm_head(args)
         return
     if args.json_mask:
         bench_json_mask(args)
@@ -446,6 +451,66 @@ def bench_lm_head(args):
                         "kernel": "lm_prep_kernel + lm_gemm_kernel (one tsm_lm_head call per step)",
                         "mfma_tflops": round(flop * (2 if split else 1) / (us * 1e-6) / 1e12, 1),
                         "mfma_peak_tflops": 2500.0},
+           "cpu_baseline": None, "oracle_check": check}
+    print(json.dumps(rec), flush=True)
+
+
+def bench_lm_head_q8(args):
+    """One step of the Q8 logits producer at the c4 shape (256 rows, dim
+    4096, vocab 151936): random int8 weights with random f16 block scales,
+    f32 activations; after the timed region the logits of four rows over
+    every id are checked bit for bit against the oracle's Q8 output layer
+    (the bar of tests/test_gpu_lmhead_q8.py)."""
+    import torch
+
+    from tachyon_amd.lmhead import lm_head_q8, workspace_bytes_q8
+
+    rows, dim, V = args.lm_rows, 4096, 151936
+    gen = torch.Generator(device="cuda").manual_seed(0x1A4F)
+    x = torch.randn(rows, dim, generator=gen, device="cuda", dtype=torch.float32) * 3.0
+    g = 1.0 + 0.2 * torch.randn(dim, generator=gen, device="cuda", dtype=torch.float32)
+    wq = torch.randint(-127, 128, (V, dim), generator=gen, device="cuda", dtype=torch.int8)
+    wsc = (0.001 * torch.randn(V, dim // 32, generator=gen, device="cuda")).to(torch.float16).view(torch.int16)
+    out = torch.empty(rows, V, dtype=torch.float32, device="cuda")
+    ws = torch.empty(workspace_bytes_q8(rows, dim), dtype=torch.uint8, device="cuda")
+    for _ in range(args.warmup):
+        lm_head_q8(x, g, 1e-6, wq, wsc, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    ea = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    eb = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for i in range(args.steps):
+        ea[i].record()
+        lm_head_q8(x, g, 1e-6, wq, wsc, out=out, workspace=ws)
+        eb[i].record()
+    torch.cuda.synchronize()
+    us = sum(ea[i].elapsed_time(eb[i]) for i in range(args.steps)) / args.steps * 1e3
+    check = None
+    if not args.no_check:
+        import numpy as np
+
+        from oracle import pyoracle
+
+        rsel = np.unique(np.array([0, rows // 3, rows - 1]))
+        rt = torch.from_numpy(rsel).cuda()
+        want = pyoracle.lm_head_q8(x[rt].cpu().numpy(), g.cpu().numpy(), 1e-6, wq.cpu().numpy(),
+                                   wsc.cpu().numpy().view(np.uint16))
+        got = out[rt].cpu().numpy()
+        check = {"rows": int(len(rsel)), "ids": V, "bit_exact": int((got.view(np.uint32) == want.view(np.uint32)).sum())}
+    alg = V * dim + V * (dim // 32) * 2 + rows * dim * 4 + dim * 4 + rows * V * 4
+    ops = 2.0 * rows * dim * V
+    rec = {"metric": "lm_head logit rows/s (rmsnorm + Q8 lm_head, dim 4096, vocab 151936)",
+           "value": round(rows / (us * 1e-6), 1), "unit": "rows/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8 weights and activations (i32 block dots, f32 scaling)",
+           "data": "synthetic",
+           "config": {"workload": f"tsm_lm_head_q8: {rows} rows x dim 4096 x vocab 151936"
+                                  + (" (the c4 batch's logits)" if rows == 256 else ""),
+                      "rows": rows, "dim": dim, "vocab": V},
+           "roofline": {"bound": "hbm", "achieved": round(alg / (us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                        "algorithmic_bytes_per_step": alg, "kernel_avg_us": round(us, 2),
+                        "kernel": "lm_q8_prep_kernel + lm_q8_gemm_kernel (one tsm_lm_head_q8 call per step)",
+                        "mfma_tops": round(ops / (us * 1e-6) / 1e12, 1), "mfma_peak_tops": 5000.0},
            "cpu_baseline": None, "oracle_check": check}
     print(json.dumps(rec), flush=True)
 

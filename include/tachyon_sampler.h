@@ -369,6 +369,25 @@ int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* no
                 const uint16_t* w, uint32_t rows, uint32_t dim, uint32_t vocab, uint32_t flags, void* workspace,
                 size_t workspace_bytes, float* logits, uint32_t ld, char* err, size_t errlen);
 
+/*
+ * The same output layer over a Q8 lm_head (weights.rs:64-70, llama.cpp's
+ * Q8_0): wq (int8 [vocab][dim], 8-byte aligned) and wscale (f16 bits
+ * [vocab][dim / 32]: one scale per block of 32 weights).  Each row of x is
+ * normalized (the sum of squares as the reference's left fold) and quantized
+ * per 32-value block (quantize_input, weights.rs:652-664, over
+ * kernels.rs:84-100); logits + r * ld receives, per vocab row, the blocks'
+ * exact integer dots, each times the weight block's scale and the row
+ * block's scale, summed in f32 in block order (the scalar dot_q8_with,
+ * kernels.rs:1420-1430).  dim is a multiple of 32 (at most TSM_LM_MAX_DIM);
+ * workspace (16-byte aligned, at least tsm_lm_head_q8_workspace bytes) is
+ * overwritten.  Replaces: lm_head.matmul for a Q8 matrix (model.rs:711-715,
+ * the Q8 arm of weights.rs:213-260).  Allocates nothing; two kernel launches.
+ */
+size_t tsm_lm_head_q8_workspace(uint32_t rows, uint32_t dim);
+int tsm_lm_head_q8(void* stream, const float* x, uint32_t x_stride, const float* norm_w, float eps, const int8_t* wq,
+                   const uint16_t* wscale, uint32_t rows, uint32_t dim, uint32_t vocab, void* workspace,
+                   size_t workspace_bytes, float* logits, uint32_t ld, char* err, size_t errlen);
+
 /* Library version string, e.g. "tachyon-sampler 0.1 gfx950". */
 const char* tsm_version(void);
 

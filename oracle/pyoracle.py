@@ -143,6 +143,11 @@ def lib():
         L.or_matmul_bf16.restype = None
         L.or_matmul_bf16.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32, vp,
                                      ctypes.c_uint32]
+        L.or_quantize_q8.restype = None
+        L.or_quantize_q8.argtypes = [vp, ctypes.c_uint32, vp, vp]
+        L.or_matmul_q8.restype = None
+        L.or_matmul_q8.argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_uint32, vp, ctypes.c_uint32, vp,
+                                   ctypes.c_uint32]
         _lib = L
     return _lib
 
@@ -396,6 +401,34 @@ def matmul_bf16(w_bits, x):
     out = np.empty((x.shape[0], rows), np.float32)
     lib().or_matmul_bf16(_vp(w_bits), rows, dim, _vp(x), x.shape[0], _vp(out), rows)
     return out
+
+
+def quantize_q8(x):
+    """quantize_q8 (kernels.rs:84-100) of one f32 row: (scales f32 [n / 32], values int8 [n])."""
+    x = np.ascontiguousarray(x, np.float32)
+    sc = np.empty(x.size // 32, np.float32)
+    q = np.empty(x.size, np.int8)
+    lib().or_quantize_q8(_vp(x), x.size, _vp(sc), _vp(q))
+    return sc, q
+
+
+def matmul_q8(wq, wscale, x):
+    """The Q8 matmul (weights.rs:474-560 over Q8Rows): each row of x (f32 [t, dim])
+    quantized per 32-value block, then out[i][r] = sum over blocks, in order, of
+    (integer block dot) * f16(wscale[r][b]) * xs[i][b].  wq int8 [rows, dim],
+    wscale f16 bit patterns u16 [rows, dim / 32]."""
+    wq = np.ascontiguousarray(wq, np.int8)
+    wscale = np.ascontiguousarray(wscale, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    rows, dim = wq.shape
+    out = np.empty((x.shape[0], rows), np.float32)
+    lib().or_matmul_q8(_vp(wq), _vp(wscale), rows, dim, _vp(x), x.shape[0], _vp(out), rows)
+    return out
+
+
+def lm_head_q8(x, norm_w, eps, wq, wscale):
+    """The output layer of model.rs:700-716 for a Q8 lm_head: rmsnorm, then the Q8 matmul."""
+    return matmul_q8(wq, wscale, rmsnorm(x, norm_w, eps))
 
 
 def lm_head(x, norm_w, eps, w_bits):

@@ -75,7 +75,8 @@ class TsmVocab(ctypes.Structure):
 SYMBOLS = ["tsm_create", "tsm_destroy", "tsm_sample", "tsm_distribution", "tsm_status", "tsm_version",
            "tsm_row_kind", "tsm_sample_static", "tsm_json_init", "tsm_json_advance", "tsm_json_accepts",
            "tsm_json_is_complete", "tsm_json_mask", "tsm_json_masks_create", "tsm_json_masks_destroy",
-           "tsm_json_masks_reset", "tsm_json_masks_fill", "tsm_lm_head_workspace", "tsm_lm_head"]
+           "tsm_json_masks_reset", "tsm_json_masks_fill", "tsm_lm_head_workspace", "tsm_lm_head",
+           "tsm_lm_head_q8_workspace", "tsm_lm_head_q8"]
 LM_SPLIT = 1
 ROWKIND_SPLIT = 1
 ROWKIND_WHOLE = 2
@@ -141,6 +142,11 @@ def lib():
         L.tsm_lm_head.restype = ctypes.c_int
         L.tsm_lm_head.argtypes = [vp, vp, u32, vp, ctypes.c_float, vp, u32, u32, u32, u32, vp, ctypes.c_size_t,
                                   vp, u32, ctypes.c_char_p, ctypes.c_size_t]
+        L.tsm_lm_head_q8_workspace.restype = ctypes.c_size_t
+        L.tsm_lm_head_q8_workspace.argtypes = [u32, u32]
+        L.tsm_lm_head_q8.restype = ctypes.c_int
+        L.tsm_lm_head_q8.argtypes = [vp, vp, u32, vp, ctypes.c_float, vp, vp, u32, u32, u32, vp, ctypes.c_size_t,
+                                     vp, u32, ctypes.c_char_p, ctypes.c_size_t]
         _lib = L
     return _lib
 

@@ -346,6 +346,340 @@ __global__ __launch_bounds__(T::kThreads) void lm_gemm_kernel(GemmArgs a) {
         }
 }
 
+// ---- the Q8 lm_head ------------------------------------------------------------
+// Tachyon's Q8 matrices (weights.rs:64-70, llama.cpp's Q8_0): per row, blocks
+// of 32 int8 values, each block with an f16 scale.  The reference quantizes
+// each activation row per 32-value block too (quantize_input, weights.rs:
+// 652-664, over kernels.rs:84-100) and sums the blocks' integer dots, each
+// times the weight block's scale and the activation block's scale, in f32
+// in block order (the scalar dot_q8_with, kernels.rs:1420-1430).
+//
+//   lm_q8_prep_kernel  one workgroup per row: the rmsnorm with the sum of
+//                      squares as the reference's left fold (the squares
+//                      computed by every thread into LDS, then added in order
+//                      by one lane), so the normalized values and their
+//                      quantization are the reference's own; then the int8
+//                      values in MFMA fragment order (q8_frag_pos) and the
+//                      block scales (q8_scale_pos), 8 lanes per block.
+//   lm_q8_gemm_kernel  the integer block dots on v_mfma_i32_16x16x64_i8, a
+//                      pair of blocks (64 bytes of a row) at a time: each
+//                      lane loads 16 contiguous weight bytes and 16
+//                      activation bytes (lane group g: bytes 16 g .. 16 g +
+//                      15 of the pair), and two MFMAs per 16 x 16 tile take
+//                      the same weight fragment against the activation
+//                      fragment with one block's lane groups (g >> 1 == h)
+//                      kept and the other's zeroed, so each MFMA sums
+//                      exactly one block's 32 products.  Each block's sum is
+//                      converted and scaled in f32 and added in block order,
+//                      as the reference does.  The
+//                      f32 work (convert, two products, a sum per row, id
+//                      and block: 4 VALU operations against 32 MACs on the
+//                      matrix cores) bounds the kernel at large batches and
+//                      the weight stream at small ones; a wave keeps the
+//                      operands of the next kQ8Ring pairs in flight in a
+//                      register ring, issued in the order they are used.
+//                      Tiles by batch size (Q8Tile): a wave owns RB row
+//                      blocks x JB id blocks of 16; WR x WN waves.
+constexpr uint32_t kQ8Block = 32;       // values per quantization block
+constexpr uint32_t kQ8Threads = 256;    // prep kernel
+constexpr uint32_t kQ8Stage = 4096;     // squares staged per round of the prep's fold
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+template <uint32_t RB_, uint32_t JB_, uint32_t WR_, uint32_t WN_, uint32_t RING_ = 3>
+struct Q8Tile {
+    static constexpr uint32_t RB = RB_, JB = JB_, WR = WR_, WN = WN_, kRing = RING_;
+    static constexpr uint32_t kRows = 16u * RB * WR, kIds = 16u * JB * WN, kThreads = 64u * WR * WN;
+};
+
+struct Q8PrepArgs {
+    const float* x;
+    const float* norm_w;
+    int8_t* aq;
+    float* as;
+    float eps;
+    uint32_t rows, rows_pad, dim, x_stride;
+};
+struct Q8GemmArgs {
+    const int8_t* aq;
+    const float* as;
+    const int8_t* wq;
+    const uint16_t* ws;
+    float* logits;
+    uint32_t rows, rows_pad, dim, vocab, ld;
+};
+
+// Byte offset of value kin (of 0..31) of block b of `row` in the
+// activations' fragment order: per 16-row block and pair of blocks (np pairs
+// a row) 1 KB, lane (row & 15) + 16 g holding bytes 16 g .. 16 g + 15 of the
+// row's pair (block 2p + (g >> 1), values 16 (g & 1) ..), the same place the
+// weight fragment holds them.
+__device__ __forceinline__ size_t q8_frag_pos(uint32_t row, uint32_t b, uint32_t kin, uint32_t np) {
+    const uint32_t g = 2u * (b & 1u) + (kin >> 4);
+    return ((static_cast<size_t>(row >> 4) * np + (b >> 1)) * 64u + (row & 15u) + 16u * g) * 16u + (kin & 15u);
+}
+
+// Index of row `row`'s scale of block b: per 16-row block and quantization
+// block, the 16 rows' scales side by side, so a lane's 4 rows are one float4.
+__device__ __forceinline__ size_t q8_scale_pos(uint32_t row, uint32_t b, uint32_t nb) {
+    return (static_cast<size_t>(row >> 4) * nb + b) * 16u + (row & 15u);
+}
+
+// f16 bits to f32 for finite values, as kernels.rs f16_finite: the bits
+// shifted into place, then scaled by 2^112.
+__device__ __forceinline__ float q8_f16(uint32_t h) {
+    const uint32_t u = ((h & 0x8000u) << 16) | ((h & 0x7FFFu) << 13);
+    return __uint_as_float(u) * __uint_as_float(0x77800000u);
+}
+
+// Rust's `(v * id).round() as i8`: halves away from zero, saturating, NaN to 0.
+__device__ __forceinline__ uint32_t q8_quant(float v, float id) {
+    const float r = roundf(v * id);
+    const int q = r != r ? 0 : r >= 127.0f ? 127 : r <= -128.0f ? -128 : static_cast<int>(r);
+    return static_cast<uint32_t>(q) & 0xFFu;
+}
+
+__global__ __launch_bounds__(kQ8Threads) void lm_q8_prep_kernel(Q8PrepArgs a) {
+    static_assert(kQ8Threads % 8u == 0 && kQ8Stage % 32u == 0, "8 lanes per block; whole blocks per stage");
+    __shared__ f32x4 sq[kQ8Stage / 4u];
+    __shared__ float inv_s;
+    const uint32_t r = blockIdx.x, tid = threadIdx.x;
+    const uint32_t nb = a.dim / kQ8Block, np = (nb + 1u) / 2u;
+    if (r >= a.rows) {  // padding rows of the last row block: every slot of the row 0
+        for (uint32_t c = tid; c < 16u * np; c += kQ8Threads)
+            *reinterpret_cast<uint32_t*>(a.aq + q8_frag_pos(r, 2u * (c >> 4) + ((c >> 3) & 1u), 4u * (c & 7u), np)) =
+                0u;
+        for (uint32_t b = tid; b < nb; b += kQ8Threads) a.as[q8_scale_pos(r, b, nb)] = 0.0f;
+        return;
+    }
+    const float* x = a.x + static_cast<size_t>(r) * a.x_stride;
+    // ss = sum of x^2 as a left fold (kernels.rs:522-528 over dot_f32): each
+    // square is rounded on its own (no fused multiply-add), so the threads
+    // form them and one lane adds them in order, a stage at a time
+    float ss = 0.0f;
+    float* sqf = reinterpret_cast<float*>(sq);
+    for (uint32_t c0 = 0; c0 < a.dim; c0 += kQ8Stage) {
+        const uint32_t len = a.dim - c0 < kQ8Stage ? a.dim - c0 : kQ8Stage;  // a multiple of 32
+        __syncthreads();
+        for (uint32_t i = tid; i < len; i += kQ8Threads) {
+            const float v = x[c0 + i];
+            sqf[i] = v * v;
+        }
+        __syncthreads();
+        if (tid == 0)
+            for (uint32_t i = 0; i < len / 4u; i += 8u) {
+                f32x4 v[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; j++) v[j] = sq[i + j];
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; j++) {
+                    ss = ss + v[j][0];
+                    ss = ss + v[j][1];
+                    ss = ss + v[j][2];
+                    ss = ss + v[j][3];
+                }
+            }
+    }
+    if (tid == 0) {
+        ss = ss / static_cast<float>(a.dim);
+        inv_s = 1.0f / sqrtf(ss + a.eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    // quantize_q8 per block (kernels.rs:84-100): 8 lanes per block, 4
+    // values each; the block's maximum |v| over the 8 lanes (a maximum of
+    // non-negative values: the same in any order)
+    const uint32_t sub = tid & 7u;
+    for (uint32_t b = tid >> 3; b < nb; b += kQ8Threads / 8u) {
+        const uint32_t k = kQ8Block * b + 4u * sub;
+        float v[4];
+        float amax = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; j++) {
+            v[j] = x[k + j] * inv * a.norm_w[k + j];
+            amax = fmaxf(amax, fabsf(v[j]));
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+        const float d = amax / 127.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        uint32_t w = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; j++) w |= q8_quant(v[j], id) << (8u * j);
+        *reinterpret_cast<uint32_t*>(a.aq + q8_frag_pos(r, b, 4u * sub, np)) = w;
+        // an odd nb's last pair has no second block: its slots hold 0
+        if (b + 1u == nb && (nb & 1u)) *reinterpret_cast<uint32_t*>(a.aq + q8_frag_pos(r, b + 1u, 4u * sub, np)) = 0u;
+        if (sub == 0) a.as[q8_scale_pos(r, b, nb)] = d;
+    }
+}
+
+// One pair of blocks' operands for a wave: per id block the weight
+// fragment (16 bytes: both blocks) and the ids' scales (f16 bits), from HBM;
+// per row block the activation fragment (16 bytes: both blocks) and the
+// rows' scales of both blocks, from L2.  A ring of T::kRing slots: the loads
+// of pair p + kRing are issued as pair p is done, weights and activations
+// together, so the waits on the load counter (which retires loads in order)
+// never hold a load that is needed later than one still in flight.  With
+// kPaired (nb even, wscale 4-byte aligned) the ids' scales come a round of
+// kQ8SRound pairs at a time, one 4-byte load per id block (lane group g:
+// pair 4t + g's two scales), passed to the other lane groups with
+// ds_bpermute; otherwise two 2-byte loads per id block and pair.
+constexpr uint32_t kQ8SRound = 4;
+constexpr uint32_t q8_lcm(uint32_t a, uint32_t b) {
+    uint32_t m = a;
+    while (m % b) m += a;
+    return m;
+}
+template <class T>
+struct Q8Slot {
+    i32x4 bf[T::JB];
+    uint32_t wsh[T::JB][2];
+    i32x4 af[T::RB];
+    f32x4 xs[T::RB][2];
+};
+
+template <class T, bool kPaired>
+__global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
+    constexpr uint32_t RB = T::RB, JB = T::JB, R = T::kRing, U = q8_lcm(T::kRing, kQ8SRound);
+    static_assert(kQ8SRound == 4, "a round's scales: one pair per lane group");
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wid = tid >> 6;
+    const uint32_t wr = wid % T::WR, wn = wid / T::WR;
+    const uint32_t nb = a.dim / kQ8Block, np = (nb + 1u) / 2u, nrb = a.rows_pad / 16u;
+    const uint32_t rb0 = blockIdx.y * (RB * T::WR) + wr * RB;           // row blocks rb0 .. rb0 + RB - 1
+    const uint32_t n0 = blockIdx.x * T::kIds + wn * (16u * JB);         // ids n0 + 16 j + (lane & 15)
+    f32x4 acc[RB][JB];
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++) acc[i][j] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};  // Rust's f32 sum starts at -0.0
+    bool rbok[RB];
+    const int8_t* abase[RB];
+    const float* sbase[RB];
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++) {
+        rbok[i] = rb0 + i < nrb;
+        const uint32_t rb = rbok[i] ? rb0 + i : 0u;
+        abase[i] = a.aq + static_cast<size_t>(rb) * np * 1024u + lane * 16u;
+        sbase[i] = a.as + static_cast<size_t>(rb) * nb * 16u + 4u * (lane >> 4);
+    }
+    bool idok[JB];
+    const int8_t* wrow[JB];
+    const uint16_t* wsrow[JB];
+#pragma unroll
+    for (uint32_t j = 0; j < JB; j++) {
+        const uint32_t id = n0 + 16u * j + (lane & 15u);
+        idok[j] = id < a.vocab;
+        const uint32_t idc = idok[j] ? id : 0u;
+        wrow[j] = a.wq + static_cast<size_t>(idc) * a.dim + 16u * (lane >> 4);
+        wsrow[j] = a.ws + static_cast<size_t>(idc) * nb;
+    }
+    const i32x4 zi = {0, 0, 0, 0};
+    const f32x4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool upper = lane >= 32u;  // lane groups 2 and 3: the pair's second block
+    // pair p: blocks 2p and, when it exists, 2p + 1 (the last pair of an odd
+    // nb has one block: lane groups 2 and 3 then load no weights, which would
+    // lie past the row's end)
+    auto load = [&](Q8Slot<T>& o, uint32_t p) {
+        const bool two = 2u * p + 1u < nb;
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++) {
+            o.bf[j] = two || !upper ? *reinterpret_cast<const i32x4*>(wrow[j] + static_cast<size_t>(p) * 64u) : zi;
+            if (!kPaired) {
+                o.wsh[j][0] = wsrow[j][2u * p];
+                o.wsh[j][1] = two ? wsrow[j][2u * p + 1u] : 0u;
+            }
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < RB; i++) {
+            const float* sp = sbase[i] + static_cast<size_t>(2u * p) * 16u;
+            o.af[i] = rbok[i] ? *reinterpret_cast<const i32x4*>(abase[i] + static_cast<size_t>(p) * 1024u) : zi;
+            o.xs[i][0] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp) : zf;
+            o.xs[i][1] = rbok[i] && two ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
+        }
+    };
+    // kPaired: the scales of pairs 4t .. 4t + 3, lane group g holding pair 4t + g's
+    auto load_s = [&](uint32_t (&sc)[JB], uint32_t t) {
+        const uint32_t p = kQ8SRound * t + (lane >> 4);
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++)
+            sc[j] = p < np ? reinterpret_cast<const uint32_t*>(wsrow[j])[p] : 0u;
+    };
+    // the scales of pair 4t + u (u the same in every lane) from lane group u
+    auto take_s = [&](Q8Slot<T>& o, const uint32_t (&sc)[JB], uint32_t u) {
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++) {
+            const uint32_t v = static_cast<uint32_t>(
+                __builtin_amdgcn_ds_bpermute(static_cast<int>(4u * ((lane & 15u) + 16u * u)), static_cast<int>(sc[j])));
+            o.wsh[j][0] = v & 0xFFFFu;
+            o.wsh[j][1] = v >> 16;
+        }
+    };
+    auto scale_add_one = [&](const Q8Slot<T>& o, uint32_t h) {
+        float wsc[JB];
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++) wsc[j] = q8_f16(o.wsh[j][h]);
+#pragma unroll
+        for (uint32_t i = 0; i < RB; i++) {
+            if (!rbok[i]) continue;
+            const i32x4 ah = (upper == (h != 0)) ? o.af[i] : zi;  // block h's lane groups only
+#pragma unroll
+            for (uint32_t j = 0; j < JB; j++) {
+                const i32x4 s = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, o.bf[j], zi, 0, 0, 0);
+#pragma unroll
+                for (uint32_t e = 0; e < 4; e++)
+                    acc[i][j][e] = acc[i][j][e] + static_cast<float>(s[e]) * wsc[j] * o.xs[i][h][e];
+            }
+        }
+    };
+    Q8Slot<T> ring[R];
+    uint32_t scur[JB], snext[JB];
+    if (kPaired) load_s(snext, 0);
+#pragma unroll
+    for (uint32_t u = 0; u < R; u++)
+        if (u < np) load(ring[u], u);
+    // U pairs a round (a multiple of the ring and of the scale round), so
+    // every slot and lane group below is fixed at compile time
+    for (uint32_t p0 = 0; p0 < np; p0 += U) {
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++) {
+            const uint32_t p = p0 + u;
+            if (p >= np) break;
+            if (kPaired && u % kQ8SRound == 0) {
+#pragma unroll
+                for (uint32_t j = 0; j < JB; j++) scur[j] = snext[j];
+                if (p + kQ8SRound < np) load_s(snext, p / kQ8SRound + 1u);
+            }
+            Q8Slot<T>& o = ring[u % R];
+            if (kPaired) take_s(o, scur, u % kQ8SRound);
+            // the pair's blocks in order
+            scale_add_one(o, 0);
+            if (2u * p + 1u < nb) scale_add_one(o, 1);
+            if (p + R < np) load(o, p + R);
+        }
+    }
+    // lane l holds rows 4 (l >> 4) + e, id l & 15 of each 16 x 16 tile
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++) {
+        if (!rbok[i]) continue;
+#pragma unroll
+        for (uint32_t e = 0; e < 4; e++) {
+            const uint32_t row = 16u * (rb0 + i) + 4u * (lane >> 4) + e;
+            if (row >= a.rows) continue;
+            float* out = a.logits + static_cast<size_t>(row) * a.ld;
+#pragma unroll
+            for (uint32_t j = 0; j < JB; j++)
+                if (idok[j]) out[n0 + 16u * j + (lane & 15u)] = acc[i][j][e];
+        }
+    }
+}
+
+template <class T>
+void launch_q8_gemm(const Q8GemmArgs& g, hipStream_t st) {
+    const dim3 grid((g.vocab + T::kIds - 1u) / T::kIds, (g.rows_pad + T::kRows - 1u) / T::kRows);
+    const bool paired = (g.dim / kQ8Block) % 2u == 0 && (reinterpret_cast<uintptr_t>(g.ws) & 3u) == 0;
+    if (paired) hipLaunchKernelGGL((lm_q8_gemm_kernel<T, true>), grid, dim3(T::kThreads), 0, st, g);
+    else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
+}
+
 void set_err(char* err, size_t errlen, const char* fmt, ...) {
     if (!err || errlen == 0) return;
     va_list ap;
@@ -429,6 +763,76 @@ int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* no
     else if (tm == 64u) launch(tsm::lm::Tile64{});
     else if (tm == 128u) launch(tsm::lm::Tile128{});
     else launch(tsm::lm::Tile256{});
+    e = hipGetLastError();
+    if (e != hipSuccess) return set_err(err, errlen, "gemm launch failed: %s", hipGetErrorString(e)), 1;
+    return 0;
+}
+
+size_t tsm_lm_head_q8_workspace(uint32_t rows, uint32_t dim) {
+    // the activation fragments (1 KB per 16 rows and pair of blocks), then
+    // the f32 block scales
+    const size_t rp = (static_cast<size_t>(rows) + 15u) / 16u * 16u, nb = dim / tsm::lm::kQ8Block;
+    return rp * ((nb + 1u) / 2u) * 64u + rp * nb * 4u;
+}
+
+int tsm_lm_head_q8(void* stream, const float* x, uint32_t x_stride, const float* norm_w, float eps, const int8_t* wq,
+                   const uint16_t* wscale, uint32_t rows, uint32_t dim, uint32_t vocab, void* workspace,
+                   size_t workspace_bytes, float* logits, uint32_t ld, char* err, size_t errlen) {
+    using tsm::lm::set_err;
+    if (rows == 0 || rows > TSM_LM_MAX_ROWS)
+        return set_err(err, errlen, "rows %u is outside [1, %u]", rows, TSM_LM_MAX_ROWS), 1;
+    if (dim == 0 || dim % tsm::lm::kQ8Block != 0 || dim > TSM_LM_MAX_DIM)
+        return set_err(err, errlen, "dim %u must be a positive multiple of %u, at most %u", dim, tsm::lm::kQ8Block,
+                       TSM_LM_MAX_DIM), 1;
+    if (vocab == 0 || vocab > TSM_MAX_VOCAB)
+        return set_err(err, errlen, "vocab %u is outside [1, %u]", vocab, TSM_MAX_VOCAB), 1;
+    if (!x || !norm_w || !wq || !wscale || !logits || !workspace)
+        return set_err(err, errlen, "x, norm_w, wq, wscale, workspace and logits must be set"), 1;
+    if (x_stride < dim) return set_err(err, errlen, "x_stride %u is below dim %u", x_stride, dim), 1;
+    if (ld < vocab) return set_err(err, errlen, "ld %u is below vocab %u", ld, vocab), 1;
+    if ((reinterpret_cast<uintptr_t>(wq) & 15u) || (reinterpret_cast<uintptr_t>(wscale) & 1u) ||
+        (reinterpret_cast<uintptr_t>(workspace) & 15u))
+        return set_err(err, errlen, "wq and workspace must be 16-byte and wscale 2-byte aligned"), 1;
+    const size_t need = tsm_lm_head_q8_workspace(rows, dim);
+    if (workspace_bytes < need)
+        return set_err(err, errlen, "workspace holds %zu bytes; %zu needed", workspace_bytes, need), 1;
+    const uint32_t rp = (rows + 15u) / 16u * 16u;
+    const size_t aqb = static_cast<size_t>(rp) * ((dim / tsm::lm::kQ8Block + 1u) / 2u) * 64u;
+    int8_t* aq = static_cast<int8_t*>(workspace);
+    float* as = reinterpret_cast<float*>(static_cast<char*>(workspace) + aqb);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+
+    tsm::lm::Q8PrepArgs p;
+    p.x = x;
+    p.norm_w = norm_w;
+    p.aq = aq;
+    p.as = as;
+    p.eps = eps;
+    p.rows = rows;
+    p.rows_pad = rp;
+    p.dim = dim;
+    p.x_stride = x_stride;
+    hipLaunchKernelGGL(tsm::lm::lm_q8_prep_kernel, dim3(rp), dim3(tsm::lm::kQ8Threads), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(err, errlen, "prep launch failed: %s", hipGetErrorString(e)), 1;
+    tsm::lm::Q8GemmArgs g;
+    g.aq = aq;
+    g.as = as;
+    g.wq = wq;
+    g.ws = wscale;
+    g.logits = logits;
+    g.rows = rows;
+    g.rows_pad = rp;
+    g.dim = dim;
+    g.vocab = vocab;
+    g.ld = ld;
+    // tiles by batch: 16 x 256, 32 x 256, 64 x 256, 128 x 128, 256 x 64 (rows x ids)
+    using namespace tsm::lm;
+    if (rp <= 16u) launch_q8_gemm<Q8Tile<1, 4, 1, 4>>(g, st);
+    else if (rp <= 32u) launch_q8_gemm<Q8Tile<2, 4, 1, 4>>(g, st);
+    else if (rp <= 64u) launch_q8_gemm<Q8Tile<2, 4, 2, 4>>(g, st);
+    else if (rp <= 128u) launch_q8_gemm<Q8Tile<2, 4, 4, 2>>(g, st);
+    else launch_q8_gemm<Q8Tile<2, 4, 8, 1>>(g, st);
     e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "gemm launch failed: %s", hipGetErrorString(e)), 1;
     return 0;

@@ -122,3 +122,26 @@ def test_lm_head_arguments_are_checked_on_the_host():
     assert call(flags=4) != 0 and b"flags" in err.value
     assert call(ws=1000) != 0 and b"workspace" in err.value
     assert call(w=ctypes.c_void_p(0x10008)) != 0 and b"aligned" in err.value
+
+
+def test_lm_head_q8_arguments_are_checked_on_the_host():
+    L = _lib.lib()
+    err = ctypes.create_string_buffer(256)
+    # workspace: the activation fragments (1 KB per 16 padded rows and pair
+    # of 32-value blocks), then one f32 scale per padded row and block
+    assert L.tsm_lm_head_q8_workspace(1, 4096) == 1 * 64 * 1024 + 16 * 128 * 4
+    assert L.tsm_lm_head_q8_workspace(17, 96) == 2 * 2 * 1024 + 32 * 3 * 4
+    assert L.tsm_lm_head_q8_workspace(3, 32) == 1 * 1 * 1024 + 16 * 1 * 4
+    fake = ctypes.c_void_p(0x10000)  # never dereferenced: every case below fails its checks first
+    def call(rows=4, dim=128, vocab=100, ws=1 << 20, ld=100, x_stride=128, w=fake, s=fake):
+        return L.tsm_lm_head_q8(None, fake, x_stride, fake, 1e-5, w, s, rows, dim, vocab, fake, ws, fake, ld,
+                                err, len(err))
+    assert call(dim=100) != 0 and b"multiple of 32" in err.value
+    assert call(rows=0) != 0 and b"rows" in err.value
+    assert call(vocab=0) != 0 and b"vocab" in err.value
+    assert call(ld=99) != 0 and b"ld" in err.value
+    assert call(x_stride=64) != 0 and b"x_stride" in err.value
+    assert call(ws=1000) != 0 and b"workspace" in err.value
+    assert call(w=ctypes.c_void_p(0x10008)) != 0 and b"aligned" in err.value
+    assert call(s=ctypes.c_void_p(0x10001)) != 0 and b"aligned" in err.value
+    assert call(w=None) != 0 and b"must be set" in err.value

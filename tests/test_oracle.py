@@ -590,3 +590,77 @@ def test_matmul_bf16_selects_and_sums_exactly(oracle):
     # (a tie) rounds to 1, 1 + 3 * 2^-8 to 1 + 2^-6
     assert _bf16_bits(np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8], np.float32)).tolist() == [0x3F80, 0x3F82]
     assert np.array_equal(_bf16_f64(_bf16_bits(np.array([1.5, -2.25], np.float32))), [1.5, -2.25])
+
+
+def test_quantize_q8_known_answers(oracle):
+    """kernels.rs:84-100: d = max|x| / 127 per 32-value block, q = (x / d)
+    rounded half away from zero.  With max|x| = 127 the scale is exactly 1,
+    so q is the rounding of x itself: the halves pin the rounding mode (half
+    to even would give 0, -2, 2 for 0.5, -2.5, 2.5), and a second block at
+    twice the size must give the same values with scale 2.  An all-zero
+    block has scale 0 and values 0; a NaN neither sets the block's maximum
+    nor survives as a value (`as i8` maps it to 0)."""
+    head = [127.0, 0.5, -0.5, 1.5, -2.5, 2.5, 63.49, -63.5, 0.49, -127.0]
+    want = [127, 1, -1, 2, -3, 3, 63, -64, 0, -127]
+    b0 = np.zeros(32, np.float32)
+    b0[:len(head)] = head
+    b3 = np.zeros(32, np.float32)
+    b3[0], b3[1], b3[2] = np.nan, 12.7, -6.35
+    x = np.concatenate([b0, 2 * b0, np.zeros(32, np.float32), b3])
+    sc, q = oracle.quantize_q8(x)
+    assert sc[:3].tolist() == [1.0, 2.0, 0.0]
+    assert np.float32(sc[3]) == np.float32(np.float32(12.7) / np.float32(127.0))
+    assert q[:len(want)].tolist() == want and not q[len(want):32].any()
+    assert np.array_equal(q[32:64], q[:32])
+    assert not q[64:96].any()
+    assert q[96:99].tolist() == [0, 127, -64] and not q[99:].any()
+
+
+def test_f16_scales_match_numpy_for_every_finite_pattern(oracle):
+    """f16_finite (kernels.rs:127-131) through the Q8 matmul: one weight row
+    per finite f16 bit pattern, holding a single 1 against an activation
+    block whose maximum is 127 (scale 1, value 127), so each logit is 127
+    times the row's f16 scale, exact in f32.  numpy's float16 conversion is
+    the check, normals, subnormals and both zeros alike."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    finite = ((bits >> 10) & 0x1F) != 0x1F
+    h = bits[finite].astype(np.uint16)
+    wq = np.zeros((h.size, 32), np.int8)
+    wq[:, 0] = 1
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 127.0
+    out = oracle.matmul_q8(wq, h[:, None], x)
+    want = h.view(np.float16).astype(np.float32) * np.float32(127.0)
+    # bit for bit, which also fixes the sign of the two zero logits: Rust's
+    # f32 sum starts at -0.0, so -0.0 + (127 * -0.0) stays -0.0 (a sum from
+    # +0.0 would give +0.0 there)
+    assert np.array_equal(out[0].view(np.uint32), want.view(np.uint32))
+    assert np.signbit(out[0][h == 0x8000]).all() and not np.signbit(out[0][h == 0]).any()
+
+
+def test_matmul_q8_exact_integer_sums(oracle):
+    """weights.rs:474-560 with Q8Rows (weights.rs:344-374) and the scalar
+    dot_q8_with (kernels.rs:1420-1430): out[i][r] = sum over blocks of the
+    block's integer dot * f16 scale * activation scale.  Activation rows
+    whose every block reaches 127 are quantized exactly (scale 1), and
+    power-of-two weight scales keep every term and sum exact in f32, so the
+    result must equal numpy's integer product with the scales applied; a
+    wrong block, row or scale index moves whole block dots."""
+    rng = np.random.default_rng(11)
+    rows, dim, t = 45, 128, 3
+    nb = dim // 32
+    wq = rng.integers(-127, 128, (rows, dim)).astype(np.int8)
+    e = rng.integers(-3, 4, (rows, nb))
+    sign = rng.choice([-1.0, 1.0], (rows, nb))
+    scale = (sign * np.exp2(e)).astype(np.float16)
+    xi = rng.integers(-60, 61, (t, dim))
+    xi[:, ::32] = 127  # each block's maximum: the activation scale is 1
+    out = oracle.matmul_q8(wq, scale.view(np.uint16), xi.astype(np.float32))
+    blocks = (wq.astype(np.int64).reshape(rows, nb, 32)[None] * xi.reshape(t, 1, nb, 32)).sum(-1)
+    want = (blocks * scale.astype(np.float64)[None]).sum(-1)
+    assert np.array_equal(out.astype(np.float64), want)
+    # an activation block of scale 2 doubles that block's share
+    x2 = xi.astype(np.float32)
+    x2[:, :32] *= 2
+    out2 = oracle.matmul_q8(wq, scale.view(np.uint16), x2)
+    assert np.array_equal(out2.astype(np.float64), want + blocks[..., 0] * scale[:, 0].astype(np.float64)[None])
