@@ -385,7 +385,7 @@ constexpr uint32_t kQ8Threads = 256;    // prep kernel
 constexpr uint32_t kQ8Stage = 4096;     // squares staged per round of the prep's fold
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-template <uint32_t RB_, uint32_t JB_, uint32_t WR_, uint32_t WN_, uint32_t RING_ = 3>
+template <uint32_t RB_, uint32_t JB_, uint32_t WR_, uint32_t WN_, uint32_t RING_ = 2>
 struct Q8Tile {
     static constexpr uint32_t RB = RB_, JB = JB_, WR = WR_, WN = WN_, kRing = RING_;
     static constexpr uint32_t kRows = 16u * RB * WR, kIds = 16u * JB * WN, kThreads = 64u * WR * WN;
@@ -519,11 +519,13 @@ __global__ __launch_bounds__(kQ8Threads) void lm_q8_prep_kernel(Q8PrepArgs a) {
 // of pair p + kRing are issued as pair p is done, weights and activations
 // together, so the waits on the load counter (which retires loads in order)
 // never hold a load that is needed later than one still in flight.  With
-// kPaired (nb even, wscale 4-byte aligned) the ids' scales come a round of
-// kQ8SRound pairs at a time, one 4-byte load per id block (lane group g:
-// pair 4t + g's two scales), passed to the other lane groups with
-// ds_bpermute; otherwise two 2-byte loads per id block and pair.
-constexpr uint32_t kQ8SRound = 4;
+// kPaired (nb a multiple of 8, wscale 16-byte aligned) the ids' scales come
+// a round of kQ8SRound pairs at a time, one 16-byte load per id block (lane
+// group g: the scales of pairs 16t + 4g .. 16t + 4g + 3), passed to the
+// other lane groups with ds_bpermute: a 128-byte line of an id's scales is
+// read by two loads, not sixteen.  Otherwise two 2-byte loads per id block
+// and pair.
+constexpr uint32_t kQ8SRound = 16;
 constexpr uint32_t q8_lcm(uint32_t a, uint32_t b) {
     uint32_t m = a;
     while (m % b) m += a;
@@ -540,7 +542,7 @@ struct Q8Slot {
 template <class T, bool kPaired>
 __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
     constexpr uint32_t RB = T::RB, JB = T::JB, R = T::kRing, U = q8_lcm(T::kRing, kQ8SRound);
-    static_assert(kQ8SRound == 4, "a round's scales: one pair per lane group");
+    static_assert(kQ8SRound == 16, "a round's scales: four pairs per lane group");
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wid = tid >> 6;
     const uint32_t wr = wid % T::WR, wn = wid / T::WR;
     const uint32_t nb = a.dim / kQ8Block, np = (nb + 1u) / 2u, nrb = a.rows_pad / 16u;
@@ -596,19 +598,22 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
             o.xs[i][1] = rbok[i] && two ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
         }
     };
-    // kPaired: the scales of pairs 4t .. 4t + 3, lane group g holding pair 4t + g's
-    auto load_s = [&](uint32_t (&sc)[JB], uint32_t t) {
-        const uint32_t p = kQ8SRound * t + (lane >> 4);
+    // kPaired: the scales of pairs 16t .. 16t + 15, lane group g holding
+    // pairs 16t + 4g .. 16t + 4g + 3 (dword d: pair 16t + 4g + d, its two
+    // blocks' scales); np is a multiple of 4, so a group's pairs all exist
+    // or none do
+    auto load_s = [&](u32x4 (&sc)[JB], uint32_t t) {
+        const uint32_t p = kQ8SRound * t + 4u * (lane >> 4);
 #pragma unroll
         for (uint32_t j = 0; j < JB; j++)
-            sc[j] = p < np ? reinterpret_cast<const uint32_t*>(wsrow[j])[p] : 0u;
+            sc[j] = p < np ? *reinterpret_cast<const u32x4*>(wsrow[j] + 2u * p) : u32x4{0u, 0u, 0u, 0u};
     };
-    // the scales of pair 4t + u (u the same in every lane) from lane group u
-    auto take_s = [&](Q8Slot<T>& o, const uint32_t (&sc)[JB], uint32_t u) {
+    // the scales of pair 16t + u (u the same in every lane) from lane group u / 4
+    auto take_s = [&](Q8Slot<T>& o, const u32x4 (&sc)[JB], uint32_t u) {
 #pragma unroll
         for (uint32_t j = 0; j < JB; j++) {
-            const uint32_t v = static_cast<uint32_t>(
-                __builtin_amdgcn_ds_bpermute(static_cast<int>(4u * ((lane & 15u) + 16u * u)), static_cast<int>(sc[j])));
+            const uint32_t v = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(
+                static_cast<int>(4u * ((lane & 15u) + 16u * (u >> 2))), static_cast<int>(sc[j][u & 3u])));
             o.wsh[j][0] = v & 0xFFFFu;
             o.wsh[j][1] = v >> 16;
         }
@@ -631,7 +636,7 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
         }
     };
     Q8Slot<T> ring[R];
-    uint32_t scur[JB], snext[JB];
+    u32x4 scur[JB], snext[JB];
     if (kPaired) load_s(snext, 0);
 #pragma unroll
     for (uint32_t u = 0; u < R; u++)
@@ -675,7 +680,7 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
 template <class T>
 void launch_q8_gemm(const Q8GemmArgs& g, hipStream_t st) {
     const dim3 grid((g.vocab + T::kIds - 1u) / T::kIds, (g.rows_pad + T::kRows - 1u) / T::kRows);
-    const bool paired = (g.dim / kQ8Block) % 2u == 0 && (reinterpret_cast<uintptr_t>(g.ws) & 3u) == 0;
+    const bool paired = (g.dim / kQ8Block) % 8u == 0 && (reinterpret_cast<uintptr_t>(g.ws) & 15u) == 0;
     if (paired) hipLaunchKernelGGL((lm_q8_gemm_kernel<T, true>), grid, dim3(T::kThreads), 0, st, g);
     else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
 }
