@@ -371,8 +371,10 @@ int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* no
 
 /*
  * The same output layer over a Q8 lm_head (weights.rs:64-70, llama.cpp's
- * Q8_0): wq (int8 [vocab][dim], 8-byte aligned) and wscale (f16 bits
- * [vocab][dim / 32]: one scale per block of 32 weights).  Each row of x is
+ * Q8_0): wq (int8 [vocab][dim], 16-byte aligned) and wscale (f16 bits
+ * [vocab][dim / 32]: one scale per block of 32 weights, 2-byte aligned;
+ * read fastest when dim is a multiple of 256 and wscale 16-byte aligned).
+ * The logits are bit-identical to the reference's scalar path.  Each row of x is
  * normalized (the sum of squares as the reference's left fold) and quantized
  * per 32-value block (quantize_input, weights.rs:652-664, over
  * kernels.rs:84-100); logits + r * ld receives, per vocab row, the blocks'
