@@ -677,12 +677,182 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
     }
 }
 
+// The paired-scale path with whole weight lines (nb a multiple of 8, wq and
+// wscale 16-byte aligned): a step is two pairs (128 bytes of each weight
+// row, one cache line), loaded 8 lanes to a row (lane: row 8h + (lane & 7),
+// bytes 16 (lane >> 3) ..) so every load reads whole lines, and turned into
+// the fragment layout through a transpose buffer of the wave's own in LDS
+// (rows padded to kQ8LineStride bytes).  A step's weights go to LDS as it
+// starts, which frees their registers for the next step's loads, issued
+// then together with the next step's activations (in the order they are
+// used, as above).
+constexpr uint32_t kQ8LineStride = 144;
+
+template <class T>
+__global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_line_kernel(Q8GemmArgs a) {
+    constexpr uint32_t RB = T::RB, JB = T::JB, W = T::kThreads / 64u;
+    __shared__ __attribute__((aligned(16))) uint8_t tbuf[W][JB][16][kQ8LineStride];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wid = tid >> 6;
+    const uint32_t wr = wid % T::WR, wn = wid / T::WR;
+    const uint32_t nb = a.dim / kQ8Block, np = nb / 2u, ns = np / 2u, nrb = a.rows_pad / 16u;
+    const uint32_t rb0 = blockIdx.y * (RB * T::WR) + wr * RB;
+    const uint32_t n0 = blockIdx.x * T::kIds + wn * (16u * JB);
+    f32x4 acc[RB][JB];
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++) acc[i][j] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};  // Rust's f32 sum starts at -0.0
+    bool rbok[RB];
+    const int8_t* abase[RB];
+    const float* sbase[RB];
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++) {
+        rbok[i] = rb0 + i < nrb;
+        const uint32_t rb = rbok[i] ? rb0 + i : 0u;
+        abase[i] = a.aq + static_cast<size_t>(rb) * np * 1024u + lane * 16u;
+        sbase[i] = a.as + static_cast<size_t>(rb) * nb * 16u + 4u * (lane >> 4);
+    }
+    bool idok[JB];
+    const uint16_t* wsrow[JB];
+    const int8_t* wline[JB][2];
+#pragma unroll
+    for (uint32_t j = 0; j < JB; j++) {
+        const uint32_t id = n0 + 16u * j + (lane & 15u);
+        idok[j] = id < a.vocab;
+        wsrow[j] = a.ws + static_cast<size_t>(idok[j] ? id : 0u) * nb;
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; h++) {
+            const uint32_t lid = n0 + 16u * j + 8u * h + (lane & 7u);
+            wline[j][h] = a.wq + static_cast<size_t>(lid < a.vocab ? lid : 0u) * a.dim + 16u * (lane >> 3);
+        }
+    }
+    uint8_t* const wbase = &tbuf[wid][0][lane & 7u][16u * (lane >> 3)];   // + j, + 8 rows for h
+    const uint8_t* const rbase = &tbuf[wid][0][lane & 15u][16u * (lane >> 4)];  // + j, + 64 bytes for t
+    const i32x4 zi = {0, 0, 0, 0};
+    const f32x4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool upper = lane >= 32u;
+
+    i32x4 wl[JB][2];
+    struct Act {
+        i32x4 af[RB][2];
+        f32x4 xs[RB][2][2];
+    };
+    auto load_w = [&](uint32_t s) {
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; h++)
+                wl[j][h] = *reinterpret_cast<const i32x4*>(wline[j][h] + static_cast<size_t>(s) * 128u);
+    };
+    auto load_a = [&](Act& x, uint32_t s) {  // step s's activations (pairs 2s, 2s + 1)
+#pragma unroll
+        for (uint32_t i = 0; i < RB; i++)
+#pragma unroll
+            for (uint32_t t = 0; t < 2u; t++) {
+                const uint32_t p = 2u * s + t;
+                const float* sp = sbase[i] + static_cast<size_t>(2u * p) * 16u;
+                x.af[i][t] = rbok[i] ? *reinterpret_cast<const i32x4*>(abase[i] + static_cast<size_t>(p) * 1024u) : zi;
+                x.xs[i][t][0] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp) : zf;
+                x.xs[i][t][1] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
+            }
+    };
+    // the scales of pairs 16r .. 16r + 15, lane group g holding pairs
+    // 16r + 4g .. 16r + 4g + 3 (np is a multiple of 4)
+    auto load_s = [&](u32x4 (&sc)[JB], uint32_t r) {
+        const uint32_t p = kQ8SRound * r + 4u * (lane >> 4);
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++)
+            sc[j] = p < np ? *reinterpret_cast<const u32x4*>(wsrow[j] + 2u * p) : u32x4{0u, 0u, 0u, 0u};
+    };
+    Act act[2];
+    u32x4 scur[JB], snext[JB];
+    load_s(snext, 0);
+    load_w(0);
+    load_a(act[0], 0);
+    // 8 steps (16 pairs, one round of scales) per iteration, so every buffer
+    // index below is fixed at compile time
+    for (uint32_t s0 = 0; s0 < ns; s0 += kQ8SRound / 2u) {
+#pragma unroll
+        for (uint32_t v = 0; v < kQ8SRound / 2u; v++) {
+            const uint32_t s = s0 + v;
+            if (s >= ns) break;
+            if (v == 0) {
+#pragma unroll
+                for (uint32_t j = 0; j < JB; j++) scur[j] = snext[j];
+                if (s0 + kQ8SRound / 2u < ns) load_s(snext, s0 / (kQ8SRound / 2u) + 1u);
+            }
+            // this step's weight lines into the transpose buffer (the
+            // previous step's reads of it have returned: their values were
+            // used), then the next step's loads
+#pragma unroll
+            for (uint32_t j = 0; j < JB; j++)
+#pragma unroll
+                for (uint32_t h = 0; h < 2u; h++)
+                    *reinterpret_cast<i32x4*>(wbase + j * (16u * kQ8LineStride) + h * (8u * kQ8LineStride)) = wl[j][h];
+            if (s + 1u < ns) {
+                load_w(s + 1u);
+                load_a(act[(v + 1u) & 1u], s + 1u);
+            }
+            const Act& x = act[v & 1u];
+#pragma unroll
+            for (uint32_t t = 0; t < 2u; t++) {
+                const uint32_t u = 2u * v + t;  // the pair's place in the scale round
+                i32x4 bf[JB];
+                float wsc[JB][2];
+#pragma unroll
+                for (uint32_t j = 0; j < JB; j++) {
+                    bf[j] = *reinterpret_cast<const i32x4*>(rbase + j * (16u * kQ8LineStride) + t * 64u);
+                    const uint32_t sv = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(
+                        static_cast<int>(4u * ((lane & 15u) + 16u * (u >> 2))), static_cast<int>(scur[j][u & 3u])));
+                    wsc[j][0] = q8_f16(sv & 0xFFFFu);
+                    wsc[j][1] = q8_f16(sv >> 16);
+                }
+#pragma unroll
+                for (uint32_t h = 0; h < 2u; h++)  // the pair's blocks in order
+#pragma unroll
+                    for (uint32_t i = 0; i < RB; i++) {
+                        if (!rbok[i]) continue;
+                        const i32x4 ah = (upper == (h != 0)) ? x.af[i][t] : zi;
+#pragma unroll
+                        for (uint32_t j = 0; j < JB; j++) {
+                            const i32x4 sm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bf[j], zi, 0, 0, 0);
+#pragma unroll
+                            for (uint32_t e = 0; e < 4; e++)
+                                acc[i][j][e] = acc[i][j][e] + static_cast<float>(sm[e]) * wsc[j][h] * x.xs[i][t][h][e];
+                        }
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++) {
+        if (!rbok[i]) continue;
+#pragma unroll
+        for (uint32_t e = 0; e < 4; e++) {
+            const uint32_t row = 16u * (rb0 + i) + 4u * (lane >> 4) + e;
+            if (row >= a.rows) continue;
+            float* out = a.logits + static_cast<size_t>(row) * a.ld;
+#pragma unroll
+            for (uint32_t j = 0; j < JB; j++)
+                if (idok[j]) out[n0 + 16u * j + (lane & 15u)] = acc[i][j][e];
+        }
+    }
+}
+
 template <class T>
 void launch_q8_gemm(const Q8GemmArgs& g, hipStream_t st) {
     const dim3 grid((g.vocab + T::kIds - 1u) / T::kIds, (g.rows_pad + T::kRows - 1u) / T::kRows);
     const bool paired = (g.dim / kQ8Block) % 8u == 0 && (reinterpret_cast<uintptr_t>(g.ws) & 15u) == 0;
-    if (paired) hipLaunchKernelGGL((lm_q8_gemm_kernel<T, true>), grid, dim3(T::kThreads), 0, st, g);
-    else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
+    // whole weight lines through LDS for the one-row-block tile (its
+    // registers leave room for a step's lines); the pair-at-a-time kernel
+    // for the others
+    if constexpr (T::RB == 1u) {
+        if (paired) hipLaunchKernelGGL((lm_q8_gemm_line_kernel<T>), grid, dim3(T::kThreads), 0, st, g);
+        else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
+    } else {
+        if (paired) hipLaunchKernelGGL((lm_q8_gemm_kernel<T, true>), grid, dim3(T::kThreads), 0, st, g);
+        else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
+    }
 }
 
 void set_err(char* err, size_t errlen, const char* fmt, ...) {
