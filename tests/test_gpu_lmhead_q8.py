@@ -148,3 +148,28 @@ def test_full_size_rows(oracle):
     want = oracle.lm_head_q8(x[pick].cpu().numpy(), g.cpu().numpy(), 1e-6, wq.cpu().numpy(),
                              ws.cpu().numpy().view(np.uint16))
     check("q8 full size", got, want)
+
+
+@pytest.mark.parametrize("rows", [7, 48])
+def test_unaligned_scales_take_the_two_byte_path(oracle, rows):
+    """Weight scales 2-byte but not 16-byte aligned (a view one element into
+    a buffer) at dim 4096: the kernels read them 2 bytes a pair instead of 16
+    pairs at a time (for 7 rows in place of whole weight lines), with the
+    same bits."""
+    import torch
+
+    from tachyon_amd.lmhead import lm_head_q8
+
+    rng = np.random.default_rng(40 + rows)
+    dim, vocab = 4096, 700
+    x = rng.normal(0, 1, (rows, dim)).astype(np.float32)
+    g = rng.normal(1.0, 0.2, dim).astype(np.float32)
+    wq, ws = weights(rng, vocab, dim)
+    buf = torch.zeros(vocab * (dim // 32) + 1, dtype=torch.int16, device="cuda")
+    buf[1:] = torch.from_numpy(ws.view(np.int16).reshape(-1)).cuda()
+    wsd = buf[1:].view(vocab, dim // 32)
+    assert wsd.data_ptr() % 16 != 0
+    say(f"q8 unaligned scales rows={rows}")
+    out = lm_head_q8(torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda(), 1e-5, torch.from_numpy(wq).cuda(), wsd)
+    torch.cuda.synchronize()
+    check(f"q8 unaligned scales {rows}", out.cpu().numpy(), oracle.lm_head_q8(x, g, 1e-5, wq, ws))
