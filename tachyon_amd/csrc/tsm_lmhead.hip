@@ -677,182 +677,169 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
     }
 }
 
-// The paired-scale path with whole weight lines (nb a multiple of 8, wq and
-// wscale 16-byte aligned): a step is two pairs (128 bytes of each weight
-// row, one cache line), loaded 8 lanes to a row (lane: row 8h + (lane & 7),
-// bytes 16 (lane >> 3) ..) so every load reads whole lines, and turned into
-// the fragment layout through a transpose buffer of the wave's own in LDS
-// (rows padded to kQ8LineStride bytes).  A step's weights go to LDS as it
-// starts, which frees their registers for the next step's loads, issued
-// then together with the next step's activations (in the order they are
-// used, as above).
-constexpr uint32_t kQ8LineStride = 144;
-
+// The paired-scale path for batches of up to 16 rows (nb a multiple of 8,
+// wq and wscale 16-byte aligned): a step is four pairs, 256 contiguous bytes
+// of each weight row (two cache lines), loaded 16 lanes to a row so that
+// every load reads whole lines, and turned into the fragment layout through
+// a transpose buffer of the wave's own in LDS (rows padded to kQ8L2Stride
+// bytes).  A step's lines go to LDS as it starts, which frees their
+// registers for the next step's loads; each pair's activations are loaded as
+// the pair two before it is done (so loads are issued in the order they are
+// used, as above).  A wave owns one row block x 2 id blocks, so that the
+// registers leave room for three waves a SIMD.
+constexpr uint32_t kQ8L2Stride = 272;
 template <class T>
 __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_line_kernel(Q8GemmArgs a) {
-    constexpr uint32_t RB = T::RB, JB = T::JB, W = T::kThreads / 64u;
-    __shared__ __attribute__((aligned(16))) uint8_t tbuf[W][JB][16][kQ8LineStride];
+    constexpr uint32_t JB = T::JB, W = T::kThreads / 64u;
+    static_assert(T::RB == 1u, "one row block a wave");
+    __shared__ __attribute__((aligned(16))) uint8_t tbuf[W][JB][16][kQ8L2Stride];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wid = tid >> 6;
-    const uint32_t wr = wid % T::WR, wn = wid / T::WR;
-    const uint32_t nb = a.dim / kQ8Block, np = nb / 2u, ns = np / 2u, nrb = a.rows_pad / 16u;
-    const uint32_t rb0 = blockIdx.y * (RB * T::WR) + wr * RB;
+    const uint32_t wn = wid / T::WR;
+    const uint32_t nb = a.dim / kQ8Block, np = nb / 2u, ns = np / 4u;
+    const uint32_t rb0 = blockIdx.y * T::WR + wid % T::WR;
     const uint32_t n0 = blockIdx.x * T::kIds + wn * (16u * JB);
-    f32x4 acc[RB][JB];
+    f32x4 acc[JB];
 #pragma unroll
-    for (uint32_t i = 0; i < RB; i++)
-#pragma unroll
-        for (uint32_t j = 0; j < JB; j++) acc[i][j] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};  // Rust's f32 sum starts at -0.0
-    bool rbok[RB];
-    const int8_t* abase[RB];
-    const float* sbase[RB];
-#pragma unroll
-    for (uint32_t i = 0; i < RB; i++) {
-        rbok[i] = rb0 + i < nrb;
-        const uint32_t rb = rbok[i] ? rb0 + i : 0u;
-        abase[i] = a.aq + static_cast<size_t>(rb) * np * 1024u + lane * 16u;
-        sbase[i] = a.as + static_cast<size_t>(rb) * nb * 16u + 4u * (lane >> 4);
-    }
+    for (uint32_t j = 0; j < JB; j++) acc[j] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
+    const bool rbok = rb0 < a.rows_pad / 16u;
+    const uint32_t rb = rbok ? rb0 : 0u;
+    const int8_t* abase = a.aq + static_cast<size_t>(rb) * np * 1024u + lane * 16u;
+    const float* sbase = a.as + static_cast<size_t>(rb) * nb * 16u + 4u * (lane >> 4);
+    // weight rows as 32-bit offsets from the workgroup's first id (a tile's
+    // rows span at most kIds * dim bytes); ids past the vocabulary read the
+    // tile's first row
+    const uint32_t t0 = blockIdx.x * T::kIds;
+    const int8_t* const wq0 = a.wq + static_cast<size_t>(t0) * a.dim;
+    const uint16_t* const ws0 = a.ws + static_cast<size_t>(t0) * nb;
     bool idok[JB];
-    const uint16_t* wsrow[JB];
-    const int8_t* wline[JB][2];
+    uint32_t wsoff[JB];
+    uint32_t wloff[JB][4];
 #pragma unroll
     for (uint32_t j = 0; j < JB; j++) {
-        const uint32_t id = n0 + 16u * j + (lane & 15u);
-        idok[j] = id < a.vocab;
-        wsrow[j] = a.ws + static_cast<size_t>(idok[j] ? id : 0u) * nb;
+        const uint32_t r = n0 - t0 + 16u * j + (lane & 15u);
+        idok[j] = t0 + r < a.vocab;
+        wsoff[j] = (idok[j] ? r : 0u) * nb;
 #pragma unroll
-        for (uint32_t h = 0; h < 2u; h++) {
-            const uint32_t lid = n0 + 16u * j + 8u * h + (lane & 7u);
-            wline[j][h] = a.wq + static_cast<size_t>(lid < a.vocab ? lid : 0u) * a.dim + 16u * (lane >> 3);
+        for (uint32_t q = 0; q < 4u; q++) {
+            const uint32_t lr = n0 - t0 + 16u * j + 4u * q + (lane >> 4);
+            wloff[j][q] = (t0 + lr < a.vocab ? lr : 0u) * a.dim + 16u * (lane & 15u);
         }
     }
-    uint8_t* const wbase = &tbuf[wid][0][lane & 7u][16u * (lane >> 3)];   // + j, + 8 rows for h
-    const uint8_t* const rbase = &tbuf[wid][0][lane & 15u][16u * (lane >> 4)];  // + j, + 64 bytes for t
+    uint8_t* const wbase = &tbuf[wid][0][lane >> 4][16u * (lane & 15u)];
+    const uint8_t* const rbase = &tbuf[wid][0][lane & 15u][16u * (lane >> 4)];
     const i32x4 zi = {0, 0, 0, 0};
     const f32x4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool upper = lane >= 32u;
-
-    i32x4 wl[JB][2];
+    i32x4 wl[JB][4];
     struct Act {
-        i32x4 af[RB][2];
-        f32x4 xs[RB][2][2];
+        i32x4 af;
+        f32x4 xs[2];
     };
     auto load_w = [&](uint32_t s) {
 #pragma unroll
         for (uint32_t j = 0; j < JB; j++)
 #pragma unroll
-            for (uint32_t h = 0; h < 2u; h++)
-                wl[j][h] = *reinterpret_cast<const i32x4*>(wline[j][h] + static_cast<size_t>(s) * 128u);
+            for (uint32_t q = 0; q < 4u; q++)
+                wl[j][q] = *reinterpret_cast<const i32x4*>(wq0 + wloff[j][q] + 256u * s);
     };
-    auto load_a = [&](Act& x, uint32_t s) {  // step s's activations (pairs 2s, 2s + 1)
-#pragma unroll
-        for (uint32_t i = 0; i < RB; i++)
-#pragma unroll
-            for (uint32_t t = 0; t < 2u; t++) {
-                const uint32_t p = 2u * s + t;
-                const float* sp = sbase[i] + static_cast<size_t>(2u * p) * 16u;
-                x.af[i][t] = rbok[i] ? *reinterpret_cast<const i32x4*>(abase[i] + static_cast<size_t>(p) * 1024u) : zi;
-                x.xs[i][t][0] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp) : zf;
-                x.xs[i][t][1] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
-            }
+    auto load_a = [&](Act& x, uint32_t p) {
+        const float* sp = sbase + static_cast<size_t>(2u * p) * 16u;
+        x.af = rbok ? *reinterpret_cast<const i32x4*>(abase + static_cast<size_t>(p) * 1024u) : zi;
+        x.xs[0] = rbok ? *reinterpret_cast<const f32x4*>(sp) : zf;
+        x.xs[1] = rbok ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
     };
-    // the scales of pairs 16r .. 16r + 15, lane group g holding pairs
-    // 16r + 4g .. 16r + 4g + 3 (np is a multiple of 4)
     auto load_s = [&](u32x4 (&sc)[JB], uint32_t r) {
         const uint32_t p = kQ8SRound * r + 4u * (lane >> 4);
 #pragma unroll
         for (uint32_t j = 0; j < JB; j++)
-            sc[j] = p < np ? *reinterpret_cast<const u32x4*>(wsrow[j] + 2u * p) : u32x4{0u, 0u, 0u, 0u};
+            sc[j] = p < np ? *reinterpret_cast<const u32x4*>(ws0 + wsoff[j] + 2u * p) : u32x4{0u, 0u, 0u, 0u};
     };
     Act act[2];
     u32x4 scur[JB], snext[JB];
     load_s(snext, 0);
     load_w(0);
     load_a(act[0], 0);
-    // 8 steps (16 pairs, one round of scales) per iteration, so every buffer
-    // index below is fixed at compile time
-    for (uint32_t s0 = 0; s0 < ns; s0 += kQ8SRound / 2u) {
+    load_a(act[1], 1);
+    for (uint32_t s0 = 0; s0 < ns; s0 += kQ8SRound / 4u) {
 #pragma unroll
-        for (uint32_t v = 0; v < kQ8SRound / 2u; v++) {
+        for (uint32_t v = 0; v < kQ8SRound / 4u; v++) {
             const uint32_t s = s0 + v;
             if (s >= ns) break;
             if (v == 0) {
 #pragma unroll
                 for (uint32_t j = 0; j < JB; j++) scur[j] = snext[j];
-                if (s0 + kQ8SRound / 2u < ns) load_s(snext, s0 / (kQ8SRound / 2u) + 1u);
+                if (s0 + kQ8SRound / 4u < ns) load_s(snext, s0 / (kQ8SRound / 4u) + 1u);
             }
-            // this step's weight lines into the transpose buffer (the
-            // previous step's reads of it have returned: their values were
-            // used), then the next step's loads
 #pragma unroll
             for (uint32_t j = 0; j < JB; j++)
 #pragma unroll
-                for (uint32_t h = 0; h < 2u; h++)
-                    *reinterpret_cast<i32x4*>(wbase + j * (16u * kQ8LineStride) + h * (8u * kQ8LineStride)) = wl[j][h];
-            if (s + 1u < ns) {
-                load_w(s + 1u);
-                load_a(act[(v + 1u) & 1u], s + 1u);
-            }
-            const Act& x = act[v & 1u];
+                for (uint32_t q = 0; q < 4u; q++)
+                    *reinterpret_cast<i32x4*>(wbase + j * (16u * kQ8L2Stride) + q * (4u * kQ8L2Stride)) = wl[j][q];
+            if (s + 1u < ns) load_w(s + 1u);
 #pragma unroll
-            for (uint32_t t = 0; t < 2u; t++) {
-                const uint32_t u = 2u * v + t;  // the pair's place in the scale round
+            for (uint32_t t = 0; t < 4u; t++) {
+                const uint32_t u = 4u * v + t;  // the pair's place in the scale round
+                const uint32_t p = 4u * s + t;
+                Act& x = act[t & 1u];
                 i32x4 bf[JB];
                 float wsc[JB][2];
 #pragma unroll
                 for (uint32_t j = 0; j < JB; j++) {
-                    bf[j] = *reinterpret_cast<const i32x4*>(rbase + j * (16u * kQ8LineStride) + t * 64u);
+                    bf[j] = *reinterpret_cast<const i32x4*>(rbase + j * (16u * kQ8L2Stride) + t * 64u);
                     const uint32_t sv = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(
                         static_cast<int>(4u * ((lane & 15u) + 16u * (u >> 2))), static_cast<int>(scur[j][u & 3u])));
                     wsc[j][0] = q8_f16(sv & 0xFFFFu);
                     wsc[j][1] = q8_f16(sv >> 16);
                 }
+                if (rbok) {
 #pragma unroll
-                for (uint32_t h = 0; h < 2u; h++)  // the pair's blocks in order
-#pragma unroll
-                    for (uint32_t i = 0; i < RB; i++) {
-                        if (!rbok[i]) continue;
-                        const i32x4 ah = (upper == (h != 0)) ? x.af[i][t] : zi;
+                    for (uint32_t h = 0; h < 2u; h++) {
+                        const i32x4 ah = (upper == (h != 0)) ? x.af : zi;
 #pragma unroll
                         for (uint32_t j = 0; j < JB; j++) {
                             const i32x4 sm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bf[j], zi, 0, 0, 0);
 #pragma unroll
                             for (uint32_t e = 0; e < 4; e++)
-                                acc[i][j][e] = acc[i][j][e] + static_cast<float>(sm[e]) * wsc[j][h] * x.xs[i][t][h][e];
+                                acc[j][e] = acc[j][e] + static_cast<float>(sm[e]) * wsc[j][h] * x.xs[h][e];
                         }
                     }
+                }
+                if (p + 2u < np) load_a(x, p + 2u);
             }
         }
     }
+    if (!rbok) return;
 #pragma unroll
-    for (uint32_t i = 0; i < RB; i++) {
-        if (!rbok[i]) continue;
+    for (uint32_t e = 0; e < 4; e++) {
+        const uint32_t row = 16u * rb0 + 4u * (lane >> 4) + e;
+        if (row >= a.rows) continue;
+        float* out = a.logits + static_cast<size_t>(row) * a.ld;
 #pragma unroll
-        for (uint32_t e = 0; e < 4; e++) {
-            const uint32_t row = 16u * (rb0 + i) + 4u * (lane >> 4) + e;
-            if (row >= a.rows) continue;
-            float* out = a.logits + static_cast<size_t>(row) * a.ld;
-#pragma unroll
-            for (uint32_t j = 0; j < JB; j++)
-                if (idok[j]) out[n0 + 16u * j + (lane & 15u)] = acc[i][j][e];
-        }
+        for (uint32_t j = 0; j < JB; j++)
+            if (idok[j]) out[n0 + 16u * j + (lane & 15u)] = acc[j][e];
     }
 }
 
-template <class T>
+// With paired scales the one-row-block tile takes the whole-line kernel
+// (its own tile: 16 rows x 128 ids), the others the pair-at-a-time kernel.
+template <class T, bool kPaired>
 void launch_q8_gemm(const Q8GemmArgs& g, hipStream_t st) {
     const dim3 grid((g.vocab + T::kIds - 1u) / T::kIds, (g.rows_pad + T::kRows - 1u) / T::kRows);
-    const bool paired = (g.dim / kQ8Block) % 8u == 0 && (reinterpret_cast<uintptr_t>(g.ws) & 15u) == 0;
-    // whole weight lines through LDS for the one-row-block tile (its
-    // registers leave room for a step's lines); the pair-at-a-time kernel
-    // for the others
-    if constexpr (T::RB == 1u) {
-        if (paired) hipLaunchKernelGGL((lm_q8_gemm_line_kernel<T>), grid, dim3(T::kThreads), 0, st, g);
-        else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
-    } else {
-        if (paired) hipLaunchKernelGGL((lm_q8_gemm_kernel<T, true>), grid, dim3(T::kThreads), 0, st, g);
-        else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, false>), grid, dim3(T::kThreads), 0, st, g);
-    }
+    if constexpr (kPaired && T::RB == 1u) hipLaunchKernelGGL((lm_q8_gemm_line_kernel<T>), grid, dim3(T::kThreads), 0, st, g);
+    else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, kPaired>), grid, dim3(T::kThreads), 0, st, g);
+}
+
+template <bool kPaired>
+void launch_q8_tiles(const Q8GemmArgs& g, hipStream_t st) {
+    // tiles by batch (rows x ids): 16 x 128 (whole lines) or 16 x 256, 32 x 256, 64 x 256, 128 x 128, 256 x 64
+    const uint32_t rp = g.rows_pad;
+    if (rp <= 16u) {
+        if constexpr (kPaired) launch_q8_gemm<Q8Tile<1, 2, 1, 4>, true>(g, st);
+        else launch_q8_gemm<Q8Tile<1, 4, 1, 4>, false>(g, st);
+    } else if (rp <= 32u) launch_q8_gemm<Q8Tile<2, 4, 1, 4>, kPaired>(g, st);
+    else if (rp <= 64u) launch_q8_gemm<Q8Tile<2, 4, 2, 4>, kPaired>(g, st);
+    else if (rp <= 128u) launch_q8_gemm<Q8Tile<2, 4, 4, 2>, kPaired>(g, st);
+    else launch_q8_gemm<Q8Tile<2, 4, 8, 1>, kPaired>(g, st);
 }
 
 void set_err(char* err, size_t errlen, const char* fmt, ...) {
@@ -1001,13 +988,12 @@ int tsm_lm_head_q8(void* stream, const float* x, uint32_t x_stride, const float*
     g.dim = dim;
     g.vocab = vocab;
     g.ld = ld;
-    // tiles by batch: 16 x 256, 32 x 256, 64 x 256, 128 x 128, 256 x 64 (rows x ids)
-    using namespace tsm::lm;
-    if (rp <= 16u) launch_q8_gemm<Q8Tile<1, 4, 1, 4>>(g, st);
-    else if (rp <= 32u) launch_q8_gemm<Q8Tile<2, 4, 1, 4>>(g, st);
-    else if (rp <= 64u) launch_q8_gemm<Q8Tile<2, 4, 2, 4>>(g, st);
-    else if (rp <= 128u) launch_q8_gemm<Q8Tile<2, 4, 4, 2>>(g, st);
-    else launch_q8_gemm<Q8Tile<2, 4, 8, 1>>(g, st);
+    // the weight scales 16 pairs at a time when dim is a multiple of 256 and
+    // wscale 16-byte aligned, else 2 bytes a pair
+    if ((dim / tsm::lm::kQ8Block) % 8u == 0 && (reinterpret_cast<uintptr_t>(wscale) & 15u) == 0)
+        tsm::lm::launch_q8_tiles<true>(g, st);
+    else
+        tsm::lm::launch_q8_tiles<false>(g, st);
     e = hipGetLastError();
     if (e != hipSuccess) return set_err(err, errlen, "gemm launch failed: %s", hipGetErrorString(e)), 1;
     return 0;
