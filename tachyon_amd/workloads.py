@@ -1,11 +1,11 @@
-"""Synthetic sampling workloads: the five BASELINE configurations and small
-random cases for parity tests.
+"""Synthetic sampling workloads: the benchmark's five configurations (c1-c5)
+and small random cases for parity tests.
 
 Each workload holds host (numpy) arrays laid out exactly as the C ABI
 expects (include/tachyon_sampler.h): logits [rows][row_stride] f32, per-row
 ``tsm_row_params`` records, CSR history, packed LSB-first masks and one
 uniform per row.  Data is synthetic (there is no model here); its shapes and
-distributions follow the BASELINE config text.
+distributions follow the benchmark configurations' descriptions.
 """
 from __future__ import annotations
 

@@ -70,7 +70,7 @@ def test_emu_parity_allowed_below_the_window(seed, rows):
 
 @pytest.mark.parametrize("name,rows", [("c1", 1), ("c2", 8), ("c3", 4), ("c4", 4), ("c5", 4)])
 def test_emu_parity_configs(name, rows):
-    """BASELINE shapes at full vocabulary with few rows.  c2's rows come in
+    """The benchmark configurations' shapes at full vocabulary with few rows.  c2's rows come in
     blocks of 8 per kind, so it takes every 4th row of the full batch to
     keep two rows of each kind."""
     if name == "c2":
