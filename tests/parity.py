@@ -1,7 +1,7 @@
 """Shared parity bars for the sampling path (GPU tests and the CPU emulation
 of the kernels compare against the CPU oracle with the same rules).
 
-Bars (BASELINE north star):
+Bars (the north-star tolerances):
 * every row: token, kept count and pick probability bit-exact with the
   reference's arithmetic (the oracle).  A row whose token or kept count
   differs passes only when the reference itself returns that pair after u

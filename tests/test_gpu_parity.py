@@ -1,7 +1,7 @@
 """GPU parity: the HIP sampling path against the CPU oracle on identical
 seeded logits, histories, masks and uniforms, through the C ABI.
 
-Bars (BASELINE north star, tests/parity.py):
+Bars (the north-star tolerances, tests/parity.py):
 * every row: token, kept count and pick probability bit-exact with the
   reference's arithmetic (rows of more than 1024 candidates included: the
   device reproduces the reference's sequential f32 folds).  A differing row
@@ -151,7 +151,7 @@ def _rows_of(w, sel, name):
 @pytest.mark.parametrize("kinds", [True, False], ids=["kinds", "nokinds"])
 def test_parity_split_path(ctx, name, kinds):
     """Batches of at most 16 rows take the split-row kernel for their top-k
-    rows: the BASELINE shapes at full vocabulary, 16 rows (c2: two of each
+    rows: the benchmark configurations' shapes at full vocabulary, 16 rows (c2: two of each
     row kind), with the batch's row kinds given and left unknown."""
     from oracle import pyoracle
     from tachyon_amd.device import run_workload
