@@ -4,7 +4,7 @@
 A step is one tsm_sample() call over one batch of synthetic logits already
 resident in HBM: one launch of the kernel that takes the batch's rows
 (topk_kernel for c3 and c4, whose rows are all of the lean kind;
-sample_kernel for c5; both for c2's mixed rows; split_kernel for c1).  The default workload is BASELINE
+sample_kernel for c5; both for c2's mixed rows; split_kernel for c1).  The default workload is the benchmark
 config c4, the headline: B=256, V=151936, repetition 1.1 + presence 0.4 +
 frequency 0.2 over 1024-token Zipf histories, a 30% grammar mask, T=0.7,
 top_k=64, top_p=0.92, min_p=0.02 and top-5 logprobs.
