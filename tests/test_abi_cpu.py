@@ -145,3 +145,25 @@ def test_lm_head_q8_arguments_are_checked_on_the_host():
     assert call(w=ctypes.c_void_p(0x10008)) != 0 and b"aligned" in err.value
     assert call(s=ctypes.c_void_p(0x10001)) != 0 and b"aligned" in err.value
     assert call(w=None) != 0 and b"must be set" in err.value
+
+
+def test_lm_head_q8_wrapper_checks_its_arguments_before_any_gpu_call():
+    """tachyon_amd.lmhead.lm_head_q8 rejects wrong dtypes, host tensors and
+    shapes that disagree before it queues anything (so this runs without a
+    GPU)."""
+    import torch
+
+    from tachyon_amd.lmhead import lm_head_q8
+
+    x = torch.zeros(2, 64)
+    g = torch.ones(64)
+    wq = torch.zeros(10, 64, dtype=torch.int8)
+    ws = torch.zeros(10, 2, dtype=torch.int16)
+    with pytest.raises(TypeError):
+        lm_head_q8(x.double(), g, 1e-5, wq, ws)
+    with pytest.raises(TypeError):
+        lm_head_q8(x, g, 1e-5, wq.to(torch.uint8), ws)
+    with pytest.raises(TypeError):
+        lm_head_q8(x, g, 1e-5, wq, ws.float())
+    with pytest.raises(ValueError, match="GPU"):
+        lm_head_q8(x, g, 1e-5, wq, ws)
