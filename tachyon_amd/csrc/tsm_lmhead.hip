@@ -677,7 +677,7 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
     }
 }
 
-// The paired-scale path for batches of up to 16 rows (nb a multiple of 8,
+// The paired-scale path for batches of up to 32 rows (nb a multiple of 8,
 // wq and wscale 16-byte aligned): a step is four pairs, 256 contiguous bytes
 // of each weight row (two cache lines), loaded 16 lanes to a row so that
 // every load reads whole lines, and turned into the fragment layout through
@@ -685,26 +685,34 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_kernel(Q8GemmArgs a) {
 // bytes).  A step's lines go to LDS as it starts, which frees their
 // registers for the next step's loads; each pair's activations are loaded as
 // the pair two before it is done (so loads are issued in the order they are
-// used, as above).  A wave owns one row block x 2 id blocks, so that the
-// registers leave room for three waves a SIMD.
+// used, as above).  A wave owns RB row blocks (1 up to 16 rows, 2 up to 32)
+// x 2 id blocks: with one row block the registers leave room for three waves
+// a SIMD.
 constexpr uint32_t kQ8L2Stride = 272;
 template <class T>
 __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_line_kernel(Q8GemmArgs a) {
-    constexpr uint32_t JB = T::JB, W = T::kThreads / 64u;
-    static_assert(T::RB == 1u, "one row block a wave");
+    constexpr uint32_t RB = T::RB, JB = T::JB, W = T::kThreads / 64u;
     __shared__ __attribute__((aligned(16))) uint8_t tbuf[W][JB][16][kQ8L2Stride];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wid = tid >> 6;
     const uint32_t wn = wid / T::WR;
     const uint32_t nb = a.dim / kQ8Block, np = nb / 2u, ns = np / 4u;
-    const uint32_t rb0 = blockIdx.y * T::WR + wid % T::WR;
+    const uint32_t rb0 = blockIdx.y * (RB * T::WR) + (wid % T::WR) * RB;  // row blocks rb0 .. rb0 + RB - 1
     const uint32_t n0 = blockIdx.x * T::kIds + wn * (16u * JB);
-    f32x4 acc[JB];
+    f32x4 acc[RB][JB];
 #pragma unroll
-    for (uint32_t j = 0; j < JB; j++) acc[j] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
-    const bool rbok = rb0 < a.rows_pad / 16u;
-    const uint32_t rb = rbok ? rb0 : 0u;
-    const int8_t* abase = a.aq + static_cast<size_t>(rb) * np * 1024u + lane * 16u;
-    const float* sbase = a.as + static_cast<size_t>(rb) * nb * 16u + 4u * (lane >> 4);
+    for (uint32_t i = 0; i < RB; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < JB; j++) acc[i][j] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
+    bool rbok[RB];
+    const int8_t* abase[RB];
+    const float* sbase[RB];
+#pragma unroll
+    for (uint32_t i = 0; i < RB; i++) {
+        rbok[i] = rb0 + i < a.rows_pad / 16u;
+        const uint32_t rb = rbok[i] ? rb0 + i : 0u;
+        abase[i] = a.aq + static_cast<size_t>(rb) * np * 1024u + lane * 16u;
+        sbase[i] = a.as + static_cast<size_t>(rb) * nb * 16u + 4u * (lane >> 4);
+    }
     // weight rows as 32-bit offsets from the workgroup's first id (a tile's
     // rows span at most kIds * dim bytes); ids past the vocabulary read the
     // tile's first row
@@ -732,8 +740,8 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_line_kernel(Q8GemmArgs
     const bool upper = lane >= 32u;
     i32x4 wl[JB][4];
     struct Act {
-        i32x4 af;
-        f32x4 xs[2];
+        i32x4 af[RB];
+        f32x4 xs[RB][2];
     };
     auto load_w = [&](uint32_t s) {
 #pragma unroll
@@ -743,10 +751,13 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_line_kernel(Q8GemmArgs
                 wl[j][q] = *reinterpret_cast<const i32x4*>(wq0 + wloff[j][q] + 256u * s);
     };
     auto load_a = [&](Act& x, uint32_t p) {
-        const float* sp = sbase + static_cast<size_t>(2u * p) * 16u;
-        x.af = rbok ? *reinterpret_cast<const i32x4*>(abase + static_cast<size_t>(p) * 1024u) : zi;
-        x.xs[0] = rbok ? *reinterpret_cast<const f32x4*>(sp) : zf;
-        x.xs[1] = rbok ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
+#pragma unroll
+        for (uint32_t i = 0; i < RB; i++) {
+            const float* sp = sbase[i] + static_cast<size_t>(2u * p) * 16u;
+            x.af[i] = rbok[i] ? *reinterpret_cast<const i32x4*>(abase[i] + static_cast<size_t>(p) * 1024u) : zi;
+            x.xs[i][0] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp) : zf;
+            x.xs[i][1] = rbok[i] ? *reinterpret_cast<const f32x4*>(sp + 16) : zf;
+        }
     };
     auto load_s = [&](u32x4 (&sc)[JB], uint32_t r) {
         const uint32_t p = kQ8SRound * r + 4u * (lane >> 4);
@@ -791,52 +802,61 @@ __global__ __launch_bounds__(T::kThreads) void lm_q8_gemm_line_kernel(Q8GemmArgs
                     wsc[j][0] = q8_f16(sv & 0xFFFFu);
                     wsc[j][1] = q8_f16(sv >> 16);
                 }
-                if (rbok) {
 #pragma unroll
-                    for (uint32_t h = 0; h < 2u; h++) {
-                        const i32x4 ah = (upper == (h != 0)) ? x.af : zi;
+                for (uint32_t h = 0; h < 2u; h++)  // the pair's blocks in order
+#pragma unroll
+                    for (uint32_t i = 0; i < RB; i++) {
+                        if (!rbok[i]) continue;
+                        const i32x4 ah = (upper == (h != 0)) ? x.af[i] : zi;
 #pragma unroll
                         for (uint32_t j = 0; j < JB; j++) {
                             const i32x4 sm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bf[j], zi, 0, 0, 0);
 #pragma unroll
                             for (uint32_t e = 0; e < 4; e++)
-                                acc[j][e] = acc[j][e] + static_cast<float>(sm[e]) * wsc[j][h] * x.xs[h][e];
+                                acc[i][j][e] = acc[i][j][e] + static_cast<float>(sm[e]) * wsc[j][h] * x.xs[i][h][e];
                         }
                     }
-                }
                 if (p + 2u < np) load_a(x, p + 2u);
             }
         }
     }
-    if (!rbok) return;
 #pragma unroll
-    for (uint32_t e = 0; e < 4; e++) {
-        const uint32_t row = 16u * rb0 + 4u * (lane >> 4) + e;
-        if (row >= a.rows) continue;
-        float* out = a.logits + static_cast<size_t>(row) * a.ld;
+    for (uint32_t i = 0; i < RB; i++) {
+        if (!rbok[i]) continue;
 #pragma unroll
-        for (uint32_t j = 0; j < JB; j++)
-            if (idok[j]) out[n0 + 16u * j + (lane & 15u)] = acc[j][e];
+        for (uint32_t e = 0; e < 4; e++) {
+            const uint32_t row = 16u * (rb0 + i) + 4u * (lane >> 4) + e;
+            if (row >= a.rows) continue;
+            float* out = a.logits + static_cast<size_t>(row) * a.ld;
+#pragma unroll
+            for (uint32_t j = 0; j < JB; j++)
+                if (idok[j]) out[n0 + 16u * j + (lane & 15u)] = acc[i][j][e];
+        }
     }
 }
 
-// With paired scales the one-row-block tile takes the whole-line kernel
-// (its own tile: 16 rows x 128 ids), the others the pair-at-a-time kernel.
+// With paired scales batches of up to 32 rows take the whole-line kernel
+// (its own tiles: 16 or 32 rows x 128 ids), the others the pair-at-a-time
+// kernel.
 template <class T, bool kPaired>
 void launch_q8_gemm(const Q8GemmArgs& g, hipStream_t st) {
     const dim3 grid((g.vocab + T::kIds - 1u) / T::kIds, (g.rows_pad + T::kRows - 1u) / T::kRows);
-    if constexpr (kPaired && T::RB == 1u) hipLaunchKernelGGL((lm_q8_gemm_line_kernel<T>), grid, dim3(T::kThreads), 0, st, g);
+    if constexpr (kPaired && T::JB == 2u) hipLaunchKernelGGL((lm_q8_gemm_line_kernel<T>), grid, dim3(T::kThreads), 0, st, g);
     else hipLaunchKernelGGL((lm_q8_gemm_kernel<T, kPaired>), grid, dim3(T::kThreads), 0, st, g);
 }
 
 template <bool kPaired>
 void launch_q8_tiles(const Q8GemmArgs& g, hipStream_t st) {
-    // tiles by batch (rows x ids): 16 x 128 (whole lines) or 16 x 256, 32 x 256, 64 x 256, 128 x 128, 256 x 64
+    // tiles by batch (rows x ids): 16 x 128 (whole lines) or 16 x 256, 32 x 128 (whole lines) or 32 x 256,
+    // 64 x 256, 128 x 128, 256 x 64
     const uint32_t rp = g.rows_pad;
     if (rp <= 16u) {
         if constexpr (kPaired) launch_q8_gemm<Q8Tile<1, 2, 1, 4>, true>(g, st);
         else launch_q8_gemm<Q8Tile<1, 4, 1, 4>, false>(g, st);
-    } else if (rp <= 32u) launch_q8_gemm<Q8Tile<2, 4, 1, 4>, kPaired>(g, st);
+    } else if (rp <= 32u) {
+        if constexpr (kPaired) launch_q8_gemm<Q8Tile<2, 2, 1, 4>, true>(g, st);
+        else launch_q8_gemm<Q8Tile<2, 4, 1, 4>, false>(g, st);
+    }
     else if (rp <= 64u) launch_q8_gemm<Q8Tile<2, 4, 2, 4>, kPaired>(g, st);
     else if (rp <= 128u) launch_q8_gemm<Q8Tile<2, 4, 4, 2>, kPaired>(g, st);
     else launch_q8_gemm<Q8Tile<2, 4, 8, 1>, kPaired>(g, st);
