@@ -381,7 +381,7 @@ __global__ __launch_bounds__(T::kThreads) void lm_gemm_kernel(GemmArgs a) {
 //                      Tiles by batch size (Q8Tile): a wave owns RB row
 //                      blocks x JB id blocks of 16; WR x WN waves.
 constexpr uint32_t kQ8Block = 32;       // values per quantization block
-constexpr uint32_t kQ8Threads = 256;    // prep kernel
+constexpr uint32_t kQ8Threads = 1024;   // prep kernel (one round of the quantization at dim 4096)
 constexpr uint32_t kQ8Stage = 4096;     // squares staged per round of the prep's fold
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
