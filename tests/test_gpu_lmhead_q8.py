@@ -173,3 +173,34 @@ def test_unaligned_scales_take_the_two_byte_path(oracle, rows):
     out = lm_head_q8(torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda(), 1e-5, torch.from_numpy(wq).cuda(), wsd)
     torch.cuda.synchronize()
     check(f"q8 unaligned scales {rows}", out.cpu().numpy(), oracle.lm_head_q8(x, g, 1e-5, wq, ws))
+
+
+def test_seeded_shape_sweep(oracle):
+    """Random shapes, bit for bit: rows 1-300 (every tile), dim a random
+    multiple of 32 up to 2048 (both ways of reading the weight scales), vocab
+    1-3000 (every tail), scales 16-byte aligned or not, random activation
+    widths.  TSM_Q8_SWEEP (environment) sets the number of cases (24)."""
+    import os
+
+    import torch
+
+    from tachyon_amd.lmhead import lm_head_q8
+
+    cases = int(os.environ.get("TSM_Q8_SWEEP", 24))
+    for k in range(cases):
+        rng = np.random.default_rng(0x0880 + k)
+        rows = int(rng.choice([1, 2, 7, 16, 17, 31, 32, 33, 64, 65, 128, 129, 256, 300]))
+        dim = 32 * int(rng.integers(1, 65))
+        vocab = int(rng.integers(1, 3001))
+        x = (rng.normal(0, 1, (rows, dim)) * np.exp(rng.normal(0, 2))).astype(np.float32)
+        g = rng.normal(1.0, 0.3, dim).astype(np.float32)
+        wq, ws = weights(rng, vocab, dim)
+        off = int(rng.integers(0, 2))
+        buf = torch.zeros(vocab * (dim // 32) + off, dtype=torch.int16, device="cuda")
+        buf[off:] = torch.from_numpy(ws.view(np.int16).reshape(-1)).cuda()
+        wsd = buf[off:].view(vocab, dim // 32)
+        out = lm_head_q8(torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda(), 1e-5, torch.from_numpy(wq).cuda(),
+                         wsd)
+        torch.cuda.synchronize()
+        check(f"q8 sweep case {k}: rows {rows} dim {dim} vocab {vocab} scale offset {off}", out.cpu().numpy(),
+              oracle.lm_head_q8(x, g, 1e-5, wq, ws))
