@@ -207,3 +207,26 @@ def test_tile_boundaries(oracle):
         want = oracle.lm_head(x, g, 1e-5, wb)
         s = bound_s(wb, oracle.rmsnorm(x, g, 1e-5))
         check(f"rows={rows} dim={dim} vocab={vocab}", run(x, g, 1e-5, wb, True), want, s, TOL_SPLIT)
+
+
+def test_seeded_shape_sweep(oracle):
+    """Random shapes against the oracle at the bounds above: rows 1-300 (every
+    tile), dim a random multiple of 64 up to 2048, vocab 1-3000 (every tail),
+    both activation modes, activation widths over a few octaves.
+    TSM_LM_SWEEP (environment) sets the number of cases (16)."""
+    import os
+
+    cases = int(os.environ.get("TSM_LM_SWEEP", 16))
+    for k in range(cases):
+        rng = np.random.default_rng(0x1A40 + k)
+        rows = int(rng.choice([1, 2, 31, 32, 33, 64, 65, 128, 129, 200, 256, 300]))
+        dim = 64 * int(rng.integers(1, 33))
+        vocab = int(rng.integers(1, 3001))
+        x = (rng.normal(0, 1, (rows, dim)) * np.exp(rng.normal(0, 2))).astype(np.float32)
+        g = rng.normal(1, 0.3, dim).astype(np.float32)
+        wb = bf16_bits(rng.normal(0, 0.05, (vocab, dim)).astype(np.float32))
+        want = oracle.lm_head(x, g, 1e-5, wb)
+        s = bound_s(wb, oracle.rmsnorm(x, g, 1e-5))
+        split = bool(k % 2)
+        case = f"lm sweep case {k}: rows {rows} dim {dim} vocab {vocab} split {split}"
+        check(case, run(x, g, 1e-5, wb, split), want, s, TOL_SPLIT if split else TOL_BF16)
