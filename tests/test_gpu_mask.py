@@ -59,19 +59,25 @@ def states_for(prefixes):
 
 
 def test_json_mask_matches_the_oracle(vocab):
+    """48 random JSON prefixes (seed 0x15A1); TSM_MASK_ROUNDS (environment)
+    adds rounds of 48 more, seeds 0x15A1 + 1, ..., for long runs."""
+    import os
+
     hv, dv = vocab
-    prefixes = wl.json_prefixes(48, seed=0x15A1)
-    cs, os_ = states_for(prefixes)
     usable = hv.n_tokens
     stride = (usable + 31) // 32 + 3  # a wider stride: the extra words are not written
-    say(f"[gpu] json mask: {len(cs)} rows x {usable} tokens")
-    got = produce(dv, cs, usable, stride)
     nw = (usable + 31) // 32
-    for r, o in enumerate(os_):
-        ref = o.mask(hv, usable)
-        bad = np.nonzero(got[r, :nw] != ref)[0]
-        assert bad.size == 0, (r, prefixes[r], bad[:5], got[r, bad[:5]], ref[bad[:5]])
-        assert (got[r, nw:] == 0x5A5A5A5A).all()
+    rounds = int(os.environ.get("TSM_MASK_ROUNDS", 1))
+    for k in range(rounds):
+        prefixes = wl.json_prefixes(48, seed=0x15A1 + k)
+        cs, os_ = states_for(prefixes)
+        say(f"[gpu] json mask round {k}: {len(cs)} rows x {usable} tokens")
+        got = produce(dv, cs, usable, stride)
+        for r, o in enumerate(os_):
+            ref = o.mask(hv, usable)
+            bad = np.nonzero(got[r, :nw] != ref)[0]
+            assert bad.size == 0, (k, r, prefixes[r], bad[:5], got[r, bad[:5]], ref[bad[:5]])
+            assert (got[r, nw:] == 0x5A5A5A5A).all()
     allowed = [int(np.unpackbits(got[r, :nw].view(np.uint8)).sum()) for r in range(len(cs))]
     say(f"[gpu] json mask: bit-exact; allowed per row min {min(allowed)} max {max(allowed)}")
 
