@@ -98,7 +98,7 @@ def test_one_hot_weights_pin_the_layout(oracle, rows):
 
 
 @pytest.mark.parametrize("rows,dim,vocab", [(1, 64, 1), (7, 128, 1000), (64, 640, 4099), (100, 192, 700),
-                                             (300, 256, 2000)])
+                                             (300, 256, 2000), (3, 8192, 500)])
 def test_random_against_the_oracle(oracle, rows, dim, vocab):
     rng = np.random.default_rng(rows * 7919 + dim + vocab)
     x = rng.normal(0, 2.0, (rows, dim)).astype(np.float32)

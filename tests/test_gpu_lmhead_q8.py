@@ -64,11 +64,13 @@ def check(case, got, want):
 
 @pytest.mark.parametrize("rows,dim,vocab", [(1, 128, 100), (20, 4096, 1000), (40, 160, 515), (100, 96, 700),
                                             (256, 512, 333), (300, 256, 4097), (17, 32, 64), (5, 224, 257),
-                                            (3, 4096, 1000), (16, 1024, 4099), (9, 768, 300), (31, 512, 777)])
+                                            (3, 4096, 1000), (16, 1024, 4099), (9, 768, 300), (31, 512, 777),
+                                            (2, 5120, 300), (40, 8192, 500)])
 def test_random_bit_exact(oracle, rows, dim, vocab):
     """Every tile shape (16, 32, 64, 128 and 256 rows; 256, 128 and 64 ids)
     with and without row and vocabulary tails, rows of 1 to 128 blocks, odd
-    counts included (the last pair of blocks then has one block), and both
+    counts included (the last pair of blocks then has one block), rows
+    longer than the prep kernel's 4096-value stage (5120, 8192), and both
     ways of reading the weight scales: 16 pairs at a time (dim a multiple of
     256; for up to 32 rows with whole weight lines through LDS) and 2 bytes
     a pair."""
