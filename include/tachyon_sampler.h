@@ -352,7 +352,7 @@ int tsm_json_masks_fill(tsm_json_masks* set, void* stream, const tsm_vocab* voca
 #define TSM_LM_MAX_DIM  32768u
 
 /* Device bytes tsm_lm_head needs as workspace for `rows` rows of `dim`
- * (the bf16 operands, rows padded to the workgroup tile: 32, 64, 128 or 256). */
+ * (the bf16 operands, rows padded to the workgroup tile: 16, 32, 64, 128 or 256). */
 size_t tsm_lm_head_workspace(uint32_t rows, uint32_t dim, uint32_t flags);
 
 /*

@@ -79,13 +79,14 @@ struct Tile {
     static_assert(kChunks * kThreads * 16 == kTileN * kStepK * 2, "weight tile split");
     static_assert(kMBlk >= 1 && kNBlk >= 1 && kRowsW % 16 == 0, "whole MFMA blocks");
 };
-// Every shape gives a wave 32 rows; fewer rows per workgroup spread the
-// waves along the vocabulary instead, so that a small batch does not pay for
-// a 256-row tile's MFMA work.
+// Every shape but the smallest gives a wave 32 rows; fewer rows per
+// workgroup spread the waves along the vocabulary instead, so that a small
+// batch does not pay for a 256-row tile's MFMA work.
 using Tile256 = Tile<256, 8, 1>;  // a wave owns 32 rows x 128 ids
 using Tile128 = Tile<128, 4, 2>;  // 32 rows x 64 ids
 using Tile64 = Tile<64, 2, 4>;    // 32 rows x 32 ids
-using Tile32 = Tile<32, 1, 8>;    // 32 rows x 16 ids (decoding)
+using Tile32 = Tile<32, 1, 8>;    // 32 rows x 16 ids
+using Tile16 = Tile<16, 1, 8>;    // 16 rows x 16 ids (decoding)
 
 struct PrepArgs {
     const float* x;
@@ -871,7 +872,9 @@ void set_err(char* err, size_t errlen, const char* fmt, ...) {
 }
 
 // The workgroup tile's rows for a batch: the smallest tile that holds it, up to 256.
-uint32_t tile_rows(uint32_t rows) { return rows <= 32u ? 32u : rows <= 64u ? 64u : rows <= 128u ? 128u : 256u; }
+uint32_t tile_rows(uint32_t rows) {
+    return rows <= 16u ? 16u : rows <= 32u ? 32u : rows <= 64u ? 64u : rows <= 128u ? 128u : 256u;
+}
 uint32_t rows_pad(uint32_t rows) { return (rows + tile_rows(rows) - 1u) / tile_rows(rows) * tile_rows(rows); }
 
 }  // namespace lm
@@ -941,7 +944,8 @@ int tsm_lm_head(void* stream, const float* x, uint32_t x_stride, const float* no
         if (split) hipLaunchKernelGGL((tsm::lm::lm_gemm_kernel<true, T>), grid, dim3(T::kThreads), 0, st, g);
         else hipLaunchKernelGGL((tsm::lm::lm_gemm_kernel<false, T>), grid, dim3(T::kThreads), 0, st, g);
     };
-    if (tm == 32u) launch(tsm::lm::Tile32{});
+    if (tm == 16u) launch(tsm::lm::Tile16{});
+    else if (tm == 32u) launch(tsm::lm::Tile32{});
     else if (tm == 64u) launch(tsm::lm::Tile64{});
     else if (tm == 128u) launch(tsm::lm::Tile128{});
     else launch(tsm::lm::Tile256{});

@@ -104,8 +104,9 @@ def test_lm_head_arguments_are_checked_on_the_host():
     L = _lib.lib()
     err = ctypes.create_string_buffer(256)
     # workspace: the bf16 operands of the rows padded to the workgroup tile
-    # (32, 64, 128 or 256 rows), twice when split
-    assert L.tsm_lm_head_workspace(1, 4096, 0) == 32 * 4096 * 2
+    # (16, 32, 64, 128 or 256 rows), twice when split
+    assert L.tsm_lm_head_workspace(1, 4096, 0) == 16 * 4096 * 2
+    assert L.tsm_lm_head_workspace(17, 4096, 0) == 32 * 4096 * 2
     assert L.tsm_lm_head_workspace(33, 4096, 0) == 64 * 4096 * 2
     assert L.tsm_lm_head_workspace(100, 4096, 0) == 128 * 4096 * 2
     assert L.tsm_lm_head_workspace(256, 4096, 0) == 256 * 4096 * 2
